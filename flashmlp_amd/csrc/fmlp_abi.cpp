@@ -1,0 +1,168 @@
+// C ABI of libflashmlp.so (declared in include/flashmlp.h): argument validation,
+// status reporting and dispatch to the gfx950 kernels. No allocation, no synchronisation.
+#include "../../include/flashmlp.h"
+#include "fmlp_launch.h"
+
+#include <hip/hip_runtime.h>
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#define FMLP_EXPORT extern "C" __attribute__((visibility("default")))
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int status, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int ok() {
+  g_last_error.clear();
+  return FMLP_OK;
+}
+
+// Compute-unit count per device, read once (device properties do not change).
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_cus[kMaxDevices];
+
+int num_cus_current(int* out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FMLP_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(FMLP_ERR_UNSUPPORTED, "device ordinal %d out of range", dev);
+  int n = g_cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    e = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return fail(FMLP_ERR_HIP, "hipDeviceGetAttribute: %s", hipGetErrorString(e));
+    if (n <= 0) n = 256;
+    g_cus[dev].store(n, std::memory_order_relaxed);
+  }
+  *out = n;
+  return FMLP_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_shape(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
+  if (H < 0 || B < 0 || D < 0 || E < 0)
+    return fail(FMLP_ERR_INVALID_ARG, "negative dimension (H=%lld B=%lld D=%lld E=%lld)", (long long)H,
+                (long long)B, (long long)D, (long long)E);
+  if (dtype != FMLP_DTYPE_F16 && dtype != FMLP_DTYPE_BF16)
+    return fail(FMLP_ERR_UNSUPPORTED, "dtype code %d: only fp16 (0) and bf16 (1) are supported", dtype);
+  if (D != 64 && D != 128) return fail(FMLP_ERR_UNSUPPORTED, "hidden dimension D=%lld: supported D are 64 and 128", (long long)D);
+  if (E < 8 || E % 8 != 0)
+    return fail(FMLP_ERR_UNSUPPORTED, "intermediate dimension E=%lld: must be a positive multiple of 8", (long long)E);
+  if (B > (1LL << 30) || E > (1LL << 30) || H > (1LL << 30))
+    return fail(FMLP_ERR_INVALID_ARG, "dimension too large (H=%lld B=%lld E=%lld)", (long long)H, (long long)B,
+                (long long)E);
+  // every tile count must fit a 32-bit grid
+  if (H * ((B + 127) / 128) + H * ((E + 127) / 128) * 64 > 0x7fffffffLL)
+    return fail(FMLP_ERR_INVALID_ARG, "problem too large for one launch");
+  return FMLP_OK;
+}
+
+int check_act(int act) {
+  if (act < FMLP_ACT_NONE || act > FMLP_ACT_SIGMOID) return fail(FMLP_ERR_INVALID_ARG, "activation code %d", act);
+  return FMLP_OK;
+}
+
+int check_ptr(const void* p, const char* name, bool needed) {
+  if (!needed) return FMLP_OK;
+  if (p == nullptr) return fail(FMLP_ERR_INVALID_ARG, "%s is NULL", name);
+  if (!aligned16(p)) return fail(FMLP_ERR_INVALID_ARG, "%s is not 16-byte aligned", name);
+  return FMLP_OK;
+}
+
+}  // namespace
+
+FMLP_EXPORT int fmlp_abi_version(void) { return FMLP_ABI_VERSION; }
+
+FMLP_EXPORT const char* fmlp_status_string(int status) {
+  switch (status) {
+    case FMLP_OK: return "ok";
+    case FMLP_ERR_INVALID_ARG: return "invalid argument";
+    case FMLP_ERR_UNSUPPORTED: return "unsupported configuration";
+    case FMLP_ERR_HIP: return "HIP runtime error";
+    case FMLP_ERR_WORKSPACE: return "workspace too small";
+    default: return "unknown status";
+  }
+}
+
+FMLP_EXPORT const char* fmlp_last_error(void) { return g_last_error.c_str(); }
+
+FMLP_EXPORT int fmlp_act_from_name(const char* name) {
+  if (name == nullptr) return FMLP_ACT_NONE;
+  if (std::strcmp(name, "silu") == 0) return FMLP_ACT_SILU;
+  if (std::strcmp(name, "leaky_relu") == 0) return FMLP_ACT_LEAKY_RELU;
+  if (std::strcmp(name, "sigmoid") == 0) return FMLP_ACT_SIGMOID;
+  return FMLP_ACT_NONE;
+}
+
+FMLP_EXPORT int fmlp_shape_supported(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
+  std::string saved = g_last_error;
+  const int st = check_shape(H, B, D, E, dtype);
+  g_last_error = saved;
+  return st == FMLP_OK ? 1 : 0;
+}
+
+FMLP_EXPORT int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
+                         int64_t E, int dtype, int act, void* stream) {
+  int st = check_shape(H, B, D, E, dtype);
+  if (st) return st;
+  if ((st = check_act(act))) return st;
+  const bool rows = H > 0 && B > 0;
+  const bool wts = H > 0;
+  if ((st = check_ptr(x, "x", rows)) || (st = check_ptr(w1, "w1", wts)) || (st = check_ptr(w2, "w2", wts)) ||
+      (st = check_ptr(o, "o", rows)))
+    return st;
+  if (!rows) return ok();
+  fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, dtype == FMLP_DTYPE_BF16, act};
+  hipError_t e = fmlp::launch_fwd(a, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(FMLP_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
+  return ok();
+}
+
+FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
+  if (check_shape(H, B, D, E, dtype) != FMLP_OK) return 0;
+  int cus = 0;
+  if (num_cus_current(&cus) != FMLP_OK) return 0;
+  return fmlp::plan_bwd(H, B, D, E, cus).ws_bytes;
+}
+
+FMLP_EXPORT int fmlp_bwd(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1,
+                         void* dw2, int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  int st = check_shape(H, B, D, E, dtype);
+  if (st) return st;
+  if ((st = check_act(act))) return st;
+  const bool rows = H > 0 && B > 0;
+  const bool wts = H > 0;
+  if ((st = check_ptr(x, "x", rows)) || (st = check_ptr(w1, "w1", wts)) || (st = check_ptr(w2, "w2", wts)) ||
+      (st = check_ptr(dout, "dout", rows)) || (st = check_ptr(dx, "dx", rows)) || (st = check_ptr(dw1, "dw1", wts)) ||
+      (st = check_ptr(dw2, "dw2", wts)))
+    return st;
+  if (H == 0) return ok();
+  int cus = 0;
+  if ((st = num_cus_current(&cus))) return st;
+  const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, cus);
+  if (plan.ws_bytes > 0) {
+    if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
+      return fail(FMLP_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, plan.ws_bytes);
+    if (!aligned16(workspace)) return fail(FMLP_ERR_INVALID_ARG, "workspace is not 16-byte aligned");
+  }
+  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, dtype == FMLP_DTYPE_BF16, act, workspace};
+  hipError_t e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  return ok();
+}

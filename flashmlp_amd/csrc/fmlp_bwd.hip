@@ -1,0 +1,564 @@
+// FlashMLP unified backward kernel for gfx950 (MI355X).
+//
+// One launch, two program roles selected by the workgroup id (flashmlp.py:360-373):
+//   * dW programs (ids [0, n_dw)): per head h, E-tile of 128 columns and a B-range. Four
+//     waves each own 32 of the E-tile's columns. X and dO rows of the B-range are streamed
+//     in 32-row subtiles through an LDS ring and used twice: row-wise as the A operand of
+//     the recomputed Z = X W1c and dH = dO W2c^T (W1c^T, W2c held in registers), and
+//     through ds_read_b64_tr_b16 as the B operand of dW2 += h^T dO and dW1^T += dZ^T X
+//     (flashmlp.py:247-329). h and dZ are cast to the io dtype before those contractions
+//     (flashmlp.py:297-320) and come straight from the MFMA C layout (lane = E column).
+//   * dX programs (ids [n_dw, n_dw + n_dx)): per head and B-tile; recompute Z^T and
+//     dH^T = W2c dO^T per 32-column E-chunk, dZ = dH * act'(Z) cast to the io dtype, and
+//     dX += dZ W1c^T (flashmlp.py:165-244). Same LDS ring and software pipeline as the
+//     forward kernel.
+// Leaky ReLU uses the autograd slope at Z == 0 (0.01); the reference Triton kernel uses 1.
+// dW programs are dispatched first (low ids): they are the long-running ones.
+#include "fmlp_device.h"
+#include "fmlp_launch.h"
+#include <type_traits>
+
+namespace fmlp {
+
+constexpr int BWD_NW = 4;            // waves per workgroup (both roles)
+constexpr int BWD_NT = BWD_NW * 64;  // threads
+constexpr int DW_ET = 128;           // E columns per dW program (32 per wave)
+constexpr int DW_BT = 32;            // rows per streamed subtile
+
+// ------------------------------------------------------------------------------------
+// dW role
+// ------------------------------------------------------------------------------------
+template <bool BF16, int D, int ACT>
+__device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __restrict__ W1,
+                                        const u16* __restrict__ W2, const u16* __restrict__ dO,
+                                        u16* __restrict__ dW1, u16* __restrict__ dW2, float* __restrict__ ws,
+                                        int H, int B, int E, int nE, int nS, int rows_per_split, int t) {
+  constexpr int KS = D / 16, NTN = D / 32;
+  constexpr unsigned SLOT = 128u * D;    // X subtile (64*D bytes) + dO subtile (64*D bytes)
+  constexpr unsigned DOOFF = 64u * D;
+  constexpr int NP = 8 * D;              // 16-byte pieces per subtile (half X, half dO)
+  constexpr int PPT = NP / BWD_NT;
+  static_assert(NP % (2 * BWD_NT) == 0, "pieces per thread");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
+  // logical order (h, s, et) with et fastest: programs streaming the same rows are adjacent
+  const int et = t % nE;
+  const int hs = t / nE;
+  const int s = hs % nS, h = hs / nS;
+  const int e_prog = et * DW_ET;
+  const int e0 = e_prog + 32 * wave;
+  const int b_lo = s * rows_per_split;
+  const int b_hi = min(B, b_lo + rows_per_split);
+  const int nsub = (b_hi - b_lo + DW_BT - 1) / DW_BT;
+
+  const u16* Xh = X + (size_t)h * B * D;
+  const u16* dOh = dO + (size_t)h * B * D;
+  const u16* W1h = W1 + (size_t)h * D * E;
+  const u16* W2h = W2 + (size_t)h * E * D;
+
+  // ---- W1c^T (B operand of Z = X W1c) via LDS: W1[:, e_prog .. +128] as [D][128] rows ----
+  {
+    constexpr int NPW = D * (DW_ET / 8);
+#pragma unroll
+    for (int k = 0; k < NPW / BWD_NT; ++k) {
+      const int p = tid + k * BWD_NT;
+      const int d = p / (DW_ET / 8), q = p % (DW_ET / 8);
+      const int e = e_prog + q * 8;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (e < E) v = *(const u32x4*)(W1h + (size_t)d * E + e);
+      lds_write16((unsigned)(d * DW_ET * 2 + q * 16), v);
+    }
+  }
+  __syncthreads();
+  u32x4 w1t[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const unsigned col = 32 * wave + 16 * (G & 1) + 4 * (i16 & 3);
+    const unsigned r0 = 16 * ks + 8 * g + (i16 >> 2);
+    w1t[ks] = cat(lds_read_tr(r0 * (DW_ET * 2) + col * 2), lds_read_tr((r0 + 4) * (DW_ET * 2) + col * 2));
+  }
+  // W2c rows (B operand of dH = dO W2c^T): lane = column e, 8 consecutive d
+  u32x4 w2r[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (e0 + l32 < E) v = *(const u32x4*)(W2h + (size_t)(e0 + l32) * D + ks * 16 + g * 8);
+    w2r[ks] = v;
+  }
+  __syncthreads();  // the W1 staging area becomes the subtile ring
+
+  // ---- subtile staging ----
+  u32x4 stg[PPT];
+  auto load_sub = [&](int k) {
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int p = tid + (j % (PPT / 2)) * BWD_NT;
+      const int r = p / (D / 8), q = p % (D / 8);
+      const int b = b_lo + k * DW_BT + r;
+      const u16* src = (j < PPT / 2) ? Xh : dOh;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (b < b_hi) v = *(const u32x4*)(src + (size_t)b * D + q * 8);
+      stg[j] = v;
+    }
+  };
+  auto store_sub = [&](int slot) {
+    const unsigned base = slot * SLOT;
+#pragma unroll
+    for (int j = 0; j < PPT; ++j) {
+      const int p = tid + (j % (PPT / 2)) * BWD_NT;
+      const int r = p / (D / 8), q = p % (D / 8);
+      lds_write16(base + (j < PPT / 2 ? 0u : DOOFF) + tile_off<D>(r, q * 8), stg[j]);
+    }
+  };
+
+  // per-lane LDS offsets (slot relative)
+  unsigned offRow[KS];  // row-wise A operand: row l32, columns 16ks + 8g
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) offRow[ks] = tile_off<D>(l32, 16 * ks + 8 * g);
+  unsigned offTr[2][2][NTN];  // transposed B operand: rows 16s + 8r + 4g + i16/4, cols 32nt + 16(G%2) + 4(i16%4)
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt)
+        offTr[s2][r][nt] = tile_off<D>(16 * s2 + 8 * r + 4 * g + (i16 >> 2), 32 * nt + 16 * (G & 1) + 4 * (i16 & 3));
+
+  f32x16 a2[NTN], a1[NTN];  // dW2 (e x d) and dW1^T (e x d) accumulators
+#pragma unroll
+  for (int nt = 0; nt < NTN; ++nt) {
+    a2[nt] = zero16();
+    a1[nt] = zero16();
+  }
+
+  auto gemm_zh = [&](int slot, f32x16& z, f32x16& dh) {
+    const unsigned base = slot * SLOT;
+    z = zero16();
+    dh = zero16();
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4 ax = lds_read16(base + offRow[ks]);
+      const u32x4 ad = lds_read16(base + DOOFF + offRow[ks]);
+      z = mfma<BF16>(ax, w1t[ks], z);
+      dh = mfma<BF16>(ad, w2r[ks], dh);
+    }
+  };
+  auto gemm_dw = [&](int slot, const u32x4 (&hT)[2], const u32x4 (&dzT)[2]) {
+    const unsigned base = slot * SLOT;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) {
+        const u32x4 bdo = cat(lds_read_tr(base + DOOFF + offTr[s2][0][nt]), lds_read_tr(base + DOOFF + offTr[s2][1][nt]));
+        a2[nt] = mfma<BF16>(hT[s2], bdo, a2[nt]);
+        const u32x4 bx = cat(lds_read_tr(base + offTr[s2][0][nt]), lds_read_tr(base + offTr[s2][1][nt]));
+        a1[nt] = mfma<BF16>(dzT[s2], bx, a1[nt]);
+      }
+  };
+  auto activate = [&](const f32x16& z, const f32x16& dh, u32x4 (&hT)[2], u32x4 (&dzT)[2]) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        float h0, d0, h1, d1;
+        act_fb<ACT>(z[8 * s2 + 2 * w], dh[8 * s2 + 2 * w], h0, d0);
+        act_fb<ACT>(z[8 * s2 + 2 * w + 1], dh[8 * s2 + 2 * w + 1], h1, d1);
+        hT[s2][w] = pack2<BF16>(h0, h1);
+        dzT[s2][w] = pack2<BF16>(d0, d1);
+      }
+  };
+
+  if (nsub > 0) {
+    load_sub(0);
+    store_sub(0);
+    if (nsub > 1) {
+      load_sub(1);
+      store_sub(1);
+    }
+    __syncthreads();
+    f32x16 zc, dhc;
+    gemm_zh(0, zc, dhc);
+    u32x4 hp[2], dzp[2];
+    auto iter = [&](auto G1, auto G2, int k) {
+      constexpr bool DO_G1 = decltype(G1)::value;
+      constexpr bool DO_G2 = decltype(G2)::value;
+      load_sub(k + 2 < nsub ? k + 2 : nsub - 1);
+      f32x16 zn, dhn;
+      if constexpr (DO_G1) gemm_zh((k + 1) & 3, zn, dhn);
+      if constexpr (DO_G2) gemm_dw((k - 1) & 3, hp, dzp);
+      activate(zc, dhc, hp, dzp);
+      store_sub((k + 2) & 3);
+      __syncthreads();
+      if constexpr (DO_G1) {
+        zc = zn;
+        dhc = dhn;
+      }
+    };
+    if (nsub == 1) {
+      activate(zc, dhc, hp, dzp);
+    } else {
+      iter(std::true_type{}, std::false_type{}, 0);
+      for (int k = 1; k < nsub - 1; ++k) iter(std::true_type{}, std::true_type{}, k);
+      iter(std::false_type{}, std::true_type{}, nsub - 1);
+    }
+    gemm_dw((nsub - 1) & 3, hp, dzp);
+  }
+
+  // ---- epilogue. C layout: lane = column d (32nt + l32), rows e = 8(i/4) + 4g + (i%4) ----
+  if (nS == 1) {
+    u16* dW2h = dW2 + (size_t)h * E * D;
+    u16* dW1h = dW1 + (size_t)h * D * E;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int eb = e0 + 8 * i4 + 4 * g;  // 4 consecutive columns eb .. eb+3 (E % 8 == 0)
+      if (eb < E) {
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) {
+          const int d = nt * 32 + l32;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dW2h[(size_t)(eb + j) * D + d] = from_f32<BF16>(a2[nt][4 * i4 + j]);
+          u32x2 v = {pack2<BF16>(a1[nt][4 * i4 + 0], a1[nt][4 * i4 + 1]), pack2<BF16>(a1[nt][4 * i4 + 2], a1[nt][4 * i4 + 3])};
+          *(u32x2*)(dW1h + (size_t)d * E + eb) = v;
+        }
+      }
+    }
+  } else {
+    // fp32 partials, both in (e, d) layout: ws2[s][h][e][d], ws1[s][h][e][d] (= dW1^T)
+    const size_t per = (size_t)H * E * D;
+    float* p2 = ws + ((size_t)s * H + h) * E * D;
+    float* p1 = ws + (size_t)nS * per + ((size_t)s * H + h) * E * D;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e = e0 + 8 * (i >> 2) + 4 * g + (i & 3);
+      if (e < E) {
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) {
+          const int d = nt * 32 + l32;
+          p2[(size_t)e * D + d] = a2[nt][i];
+          p1[(size_t)e * D + d] = a1[nt][i];
+        }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// dX role
+// ------------------------------------------------------------------------------------
+template <bool BF16, int D, int ACT, int MT>
+__device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __restrict__ W1,
+                                        const u16* __restrict__ W2, const u16* __restrict__ dO,
+                                        u16* __restrict__ dX, int B, int E, int tiles_per_head, int t) {
+  constexpr int KS = D / 16, NTN = D / 32;
+  constexpr int BB = BWD_NW * MT * 32;
+  constexpr unsigned SLOT = 128u * D;
+  constexpr unsigned W2OFF = 64u * D;
+  constexpr int NP = 8 * D;
+  constexpr int PPT = NP / BWD_NT;
+  static_assert(NP % (2 * BWD_NT) == 0, "pieces per thread");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
+  const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
+  const int NC = (E + 31) >> 5;
+
+  const u16* Xh = X + (size_t)h * B * D;
+  const u16* dOh = dO + (size_t)h * B * D;
+  const u16* W1h = W1 + (size_t)h * D * E;
+  const u16* W2h = W2 + (size_t)h * E * D;
+  u16* dXh = dX + (size_t)h * B * D;
+  const int b_wave = bt * BB + wave * MT * 32;
+
+  u32x4 stg[PPT];
+  auto load_chunk = [&](int c) {
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (k < PPT / 2) {
+        const int p = tid + k * BWD_NT;
+        const int d = p >> 2, q = p & 3;
+        const int e = c * 32 + q * 8;
+        if (e < E) v = *(const u32x4*)(W1h + (size_t)d * E + e);
+      } else {
+        const int p = tid + (k - PPT / 2) * BWD_NT;
+        const int er = p / (D / 8), q = p % (D / 8);
+        const int e = c * 32 + er;
+        if (e < E) v = *(const u32x4*)(W2h + (size_t)e * D + q * 8);
+      }
+      stg[k] = v;
+    }
+  };
+  auto store_chunk = [&](int slot) {
+    const unsigned base = slot * SLOT;
+#pragma unroll
+    for (int k = 0; k < PPT; ++k) {
+      if (k < PPT / 2) {
+        const int p = tid + k * BWD_NT;
+        const int d = p >> 2, q = p & 3;
+        u32x2 lo = {stg[k][0], stg[k][1]}, hi = {stg[k][2], stg[k][3]};
+        lds_write8(base + w1c_off(d, 2 * q), lo);
+        lds_write8(base + w1c_off(d, 2 * q + 1), hi);
+      } else {
+        const int p = tid + (k - PPT / 2) * BWD_NT;
+        const int er = p / (D / 8), q = p % (D / 8);
+        lds_write16(base + W2OFF + tile_off<D>(er, q * 8), stg[k]);
+      }
+    }
+  };
+
+  // X and dO rows in registers: B operand (lane = row b, 8 consecutive d)
+  u32x4 xr[MT][KS], dr[MT][KS];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int b = b_wave + mt * 32 + l32;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 v = {0u, 0u, 0u, 0u}, w = {0u, 0u, 0u, 0u};
+      if (b < B) {
+        v = *(const u32x4*)(Xh + (size_t)b * D + ks * 16 + g * 8);
+        w = *(const u32x4*)(dOh + (size_t)b * D + ks * 16 + g * 8);
+      }
+      xr[mt][ks] = v;
+      dr[mt][ks] = w;
+    }
+  }
+
+  unsigned offA[2][2];  // tr read of W1c (A operand of Z^T)
+#pragma unroll
+  for (int kp = 0; kp < 2; ++kp)
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+      offA[kp][r] = w1c_off(16 * kp + 8 * g + 4 * r + (i16 >> 2), 4 * (G & 1) + (i16 & 3));
+  unsigned offW2[KS];  // row-wise read of W2c (A operand of dH^T): row l32, columns 16ks + 8g
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) offW2[ks] = W2OFF + tile_off<D>(l32, 16 * ks + 8 * g);
+  unsigned offW1[2][2][NTN];  // 8-byte reads of W1c (B operand of dX): row 32nt + l32, unit 4s + 2r + g
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) offW1[s2][r][nt] = w1c_off(32 * nt + l32, 4 * s2 + 2 * r + g);
+
+  f32x16 acc[MT][NTN];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NTN; ++nt) acc[mt][nt] = zero16();
+
+  auto gemm_zh = [&](int slot, f32x16 (&z)[MT], f32x16 (&dh)[MT]) {
+    const unsigned base = slot * SLOT;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      z[mt] = zero16();
+      dh[mt] = zero16();
+    }
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const u32x4 A = cat(lds_read_tr(base + offA[ks & 1][0] + (ks >> 1) * 2048u),
+                          lds_read_tr(base + offA[ks & 1][1] + (ks >> 1) * 2048u));
+      const u32x4 A2 = lds_read16(base + offW2[ks]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        z[mt] = mfma<BF16>(A, xr[mt][ks], z[mt]);
+        dh[mt] = mfma<BF16>(A2, dr[mt][ks], dh[mt]);
+      }
+    }
+  };
+  auto gemm_dx = [&](int slot, const u32x4 (&dzA)[MT][2]) {
+    const unsigned base = slot * SLOT;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) {
+        const u32x4 Bv = cat(lds_read8(base + offW1[s2][0][nt]), lds_read8(base + offW1[s2][1][nt]));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma<BF16>(dzA[mt][s2], Bv, acc[mt][nt]);
+      }
+  };
+  auto activate = [&](const f32x16 (&z)[MT], const f32x16 (&dh)[MT], u32x4 (&dzA)[MT][2]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          dzA[mt][s2][w] = pack2<BF16>(act_b<ACT>(z[mt][8 * s2 + 2 * w], dh[mt][8 * s2 + 2 * w]),
+                                       act_b<ACT>(z[mt][8 * s2 + 2 * w + 1], dh[mt][8 * s2 + 2 * w + 1]));
+  };
+
+  load_chunk(0);
+  store_chunk(0);
+  if (NC > 1) {
+    load_chunk(1);
+    store_chunk(1);
+  }
+  __syncthreads();
+  f32x16 zc[MT], dhc[MT];
+  gemm_zh(0, zc, dhc);
+  u32x4 dzp[MT][2];
+  auto iter = [&](auto G1, auto G2, int c) {
+    constexpr bool DO_G1 = decltype(G1)::value;
+    constexpr bool DO_G2 = decltype(G2)::value;
+    load_chunk(c + 2 < NC ? c + 2 : NC - 1);
+    f32x16 zn[MT], dhn[MT];
+    if constexpr (DO_G1) gemm_zh((c + 1) & 3, zn, dhn);
+    if constexpr (DO_G2) gemm_dx((c - 1) & 3, dzp);
+    activate(zc, dhc, dzp);
+    store_chunk((c + 2) & 3);
+    __syncthreads();
+    if constexpr (DO_G1) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        zc[mt] = zn[mt];
+        dhc[mt] = dhn[mt];
+      }
+    }
+  };
+  if (NC == 1) {
+    activate(zc, dhc, dzp);
+  } else {
+    iter(std::true_type{}, std::false_type{}, 0);
+    for (int c = 1; c < NC - 1; ++c) iter(std::true_type{}, std::true_type{}, c);
+    iter(std::false_type{}, std::true_type{}, NC - 1);
+  }
+  gemm_dx((NC - 1) & 3, dzp);
+
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int b = b_wave + mt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
+      if (b < B) {
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) dXh[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(acc[mt][nt][i]);
+      }
+    }
+}
+
+template <bool BF16, int D, int ACT, int MT>
+__global__ void __launch_bounds__(BWD_NT)
+bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+           const u16* __restrict__ dO, u16* __restrict__ dX, u16* __restrict__ dW1, u16* __restrict__ dW2,
+           float* __restrict__ ws, int H, int B, int E, int nE, int nS, int rows_per_split, int n_dw,
+           int dx_tiles_per_head) {
+  const int bid = blockIdx.x;
+  if (bid < n_dw) {
+    dw_role<BF16, D, ACT>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, xcd_remap(bid, n_dw));
+  } else {
+    const int n_dx = (int)gridDim.x - n_dw;
+    dx_role<BF16, D, ACT, MT>(X, W1, W2, dO, dX, B, E, dx_tiles_per_head, xcd_remap(bid - n_dw, n_dx));
+  }
+}
+
+// Sum of the nS fp32 partials; dW2 keeps the (e, d) layout, dW1 is written transposed.
+template <bool BF16>
+__global__ void __launch_bounds__(256)
+dw_reduce_kernel(const float* __restrict__ ws, u16* __restrict__ dW1, u16* __restrict__ dW2, int H, int E, int D,
+                 int nS) {
+  const size_t per = (size_t)H * E * D;
+  const size_t stride = (size_t)gridDim.x * blockDim.x;
+  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < per; idx += stride) {
+    // dW2[h][e][d]
+    float s2 = 0.f;
+    for (int s = 0; s < nS; ++s) s2 += ws[(size_t)s * per + idx];
+    dW2[idx] = from_f32<BF16>(s2);
+    // dW1[h][d][e] from ws1[s][h][e][d]
+    const size_t h = idx / ((size_t)D * E);
+    const size_t rem = idx - h * (size_t)D * E;
+    const size_t d = rem / E, e = rem - d * E;
+    const size_t src = (h * E + e) * D + d;
+    float s1 = 0.f;
+    for (int s = 0; s < nS; ++s) s1 += ws[(size_t)(nS + s) * per + src];
+    dW1[idx] = from_f32<BF16>(s1);
+  }
+}
+
+// ------------------------------------------------------------------------------------
+// host side
+// ------------------------------------------------------------------------------------
+BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus) {
+  BwdPlan p{};
+  p.nE = (int)((E + DW_ET - 1) / DW_ET);
+  const long long base = H * (long long)p.nE;
+  // B splits so that the dW programs alone cover every CU; each split keeps >= 256 rows.
+  long long ns = base > 0 ? (num_cus + base - 1) / base : 1;
+  const long long max_ns = B / 256 > 1 ? B / 256 : 1;
+  if (ns > max_ns) ns = max_ns;
+  if (ns < 1) ns = 1;
+  long long rps = (B + ns - 1) / ns;
+  rps = (rps + DW_BT - 1) / DW_BT * DW_BT;
+  if (rps < DW_BT) rps = DW_BT;
+  ns = (B + rps - 1) / rps;
+  if (ns < 1) ns = 1;
+  p.nS = (int)ns;
+  p.rows_per_split = (int)rps;
+  // dX programs: 256 rows when that still gives >= 2 programs per CU, else 128
+  // (D = 128 with two M-tiles per wave exceeds the register file, so it keeps one)
+  const long long big = (B + 255) / 256 * H;
+  p.dx_mt = (D == 64 && big >= 2LL * num_cus) ? 2 : 1;
+  const int rows = BWD_NW * 32 * p.dx_mt;
+  p.dx_tiles_per_head = (int)((B + rows - 1) / rows);
+  p.n_dw = base * p.nS;
+  p.n_dx = (long long)p.dx_tiles_per_head * H;
+  p.ws_bytes = p.nS > 1 ? (size_t)2 * p.nS * H * E * D * sizeof(float) : 0;
+  return p;
+}
+
+template <bool BF16, int D, int ACT>
+static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
+  const long long grid = p.n_dw + p.n_dx;
+  if (grid <= 0) return hipSuccess;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  const size_t lds_dw = 4u * 128u * D > (size_t)D * DW_ET * 2 ? 4u * 128u * D : (size_t)D * DW_ET * 2;
+  const size_t lds = lds_dw;  // the dX ring (4 * 128 * D) is the same size
+  hipError_t e;
+  if (D == 64 && p.dx_mt == 2) {
+    auto k = bwd_kernel<BF16, D, ACT, (D == 64 ? 2 : 1)>;
+    e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(BWD_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                       (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dx, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws,
+                       (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw, p.dx_tiles_per_head);
+  } else {
+    auto k = bwd_kernel<BF16, D, ACT, 1>;
+    e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(BWD_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                       (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dx, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws,
+                       (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw, p.dx_tiles_per_head);
+  }
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.nS > 1) {
+    const size_t per = (size_t)a.H * a.E * a.D;
+    size_t blocks = (per + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws,
+                       (u16*)a.dw1, (u16*)a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+template <bool BF16, int D>
+static hipError_t launch_bwd_a(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
+  switch (a.act) {
+    case ACT_SILU: return launch_bwd_t<BF16, D, ACT_SILU>(a, p, st);
+    case ACT_LEAKY: return launch_bwd_t<BF16, D, ACT_LEAKY>(a, p, st);
+    case ACT_SIGMOID: return launch_bwd_t<BF16, D, ACT_SIGMOID>(a, p, st);
+    default: return launch_bwd_t<BF16, D, ACT_NONE>(a, p, st);
+  }
+}
+
+hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
+  if (a.bf16) {
+    if (a.D == 128) return launch_bwd_a<true, 128>(a, p, st);
+    return launch_bwd_a<true, 64>(a, p, st);
+  }
+  if (a.D == 128) return launch_bwd_a<false, 128>(a, p, st);
+  return launch_bwd_a<false, 64>(a, p, st);
+}
+
+}  // namespace fmlp

@@ -1,0 +1,203 @@
+// Device-side building blocks shared by the FlashMLP gfx950 kernels.
+//
+// Conventions (all kernels):
+//   * io element type is 16-bit (fp16 or bf16) held as `u16` in memory;
+//   * every dense contraction is a v_mfma_f32_32x32x16_{bf16,f16} with fp32 accumulation;
+//   * MFMA 32x32x16 lane layout (verified on MI355X):
+//       A (M x K): lane l holds row m = l%32, k-slots 8*(l/32) + j, j = 0..7
+//       B (K x N): lane l holds col n = l%32, k-slots 8*(l/32) + j
+//       C (M x N): lane l holds col n = l%32, rows m = 8*(i/4) + 4*(l/32) + (i%4), i = 0..15
+//     Only the pairing of A and B k-slots matters (a contraction is order free), so an
+//     operand built from a C tile keeps the C row order as its k order and the other
+//     operand is read with the same permutation.
+//   * ds_read_b64_tr_b16 (verified): within each 16-lane group, lane i receives element
+//     (i % 4) of the 8 bytes read by lanes 4*j + i/4, j = 0..3. Reading a 4x16 block of a
+//     row-major 16-bit matrix (lane i reads row i/4, columns 4*(i%4)..+3) therefore gives
+//     lane i column i, rows 0..3: a K-contiguous operand from an N-contiguous layout.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace fmlp {
+
+typedef unsigned short u16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+#define FMLP_LDS __attribute__((address_space(3)))
+
+enum Act { ACT_NONE = 0, ACT_SILU = 1, ACT_LEAKY = 2, ACT_SIGMOID = 3 };
+
+// 8 x 16-bit operand held as four dwords.
+struct Frag { u32x4 v; };
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+template <bool BF16>
+__device__ __forceinline__ f32x16 mfma(const u32x4& a, const u32x4& b, const f32x16& c) {
+  if constexpr (BF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// Round-to-nearest-even conversion of two fp32 values into one dword of 16-bit values
+// (low half = a). Lowers to v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32 on gfx950.
+template <bool BF16>
+__device__ __forceinline__ unsigned pack2(float a, float b) {
+  if constexpr (BF16) {
+    bf16x2 v = {(__bf16)a, (__bf16)b};
+    return __builtin_bit_cast(unsigned, v);
+  } else {
+    f16x2 v = {(_Float16)a, (_Float16)b};
+    return __builtin_bit_cast(unsigned, v);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ float to_f32(u16 h) {
+  if constexpr (BF16) {
+    return __uint_as_float(((unsigned)h) << 16);
+  } else {
+    return (float)__builtin_bit_cast(_Float16, h);
+  }
+}
+
+template <bool BF16>
+__device__ __forceinline__ u16 from_f32(float f) {
+  return (u16)(pack2<BF16>(f, 0.f) & 0xffffu);
+}
+
+// ---------------------------------------------------------------------------------
+// Activations. Follows flashmlp.py:27-46 (forward) and PyTorch autograd for the
+// derivatives (flashmlp.py:671-686 is differentiated by autograd in the oracle):
+//   leaky(z) = z > 0 ? z : 0.01 z        leaky'(z) = z > 0 ? 1 : 0.01   (autograd at z == 0)
+//   silu(z)  = z * s(z)                  silu'(z) = s + h (1 - s), h = z s (fp32)
+//   sigmoid(z) = s(z)                    sigmoid'(z) = s (1 - s)
+// s(z) = 1 / (1 + 2^(-z * log2 e)) : the definition of the logistic function with
+// e^x = 2^(x log2 e); v_exp_f32 and v_rcp_f32 are the hardware base-2 exponential and
+// reciprocal (each accurate to about 1 ulp).
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ float sigm(float z) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(z * -1.4426950408889634f));
+}
+
+template <int ACT>
+__device__ __forceinline__ float act_f(float z) {
+  if constexpr (ACT == ACT_SILU) return z * sigm(z);
+  else if constexpr (ACT == ACT_LEAKY) return z > 0.f ? z : 0.01f * z;
+  else if constexpr (ACT == ACT_SIGMOID) return sigm(z);
+  else return z;
+}
+
+// h = act(z) and dz = dh * act'(z)
+template <int ACT>
+__device__ __forceinline__ void act_fb(float z, float dh, float& h, float& dz) {
+  if constexpr (ACT == ACT_SILU) {
+    float s = sigm(z);
+    h = z * s;
+    dz = dh * __builtin_fmaf(h, 1.0f - s, s);
+  } else if constexpr (ACT == ACT_LEAKY) {
+    bool p = z > 0.f;
+    h = p ? z : 0.01f * z;
+    dz = p ? dh : 0.01f * dh;
+  } else if constexpr (ACT == ACT_SIGMOID) {
+    float s = sigm(z);
+    h = s;
+    dz = dh * (s - s * s);
+  } else {
+    h = z;
+    dz = dh;
+  }
+}
+
+// dz only (dX programs never need h)
+template <int ACT>
+__device__ __forceinline__ float act_b(float z, float dh) {
+  if constexpr (ACT == ACT_SILU) {
+    float s = sigm(z);
+    float h = z * s;
+    return dh * __builtin_fmaf(h, 1.0f - s, s);
+  } else if constexpr (ACT == ACT_LEAKY) {
+    return z > 0.f ? dh : 0.01f * dh;
+  } else if constexpr (ACT == ACT_SIGMOID) {
+    float s = sigm(z);
+    return dh * (s - s * s);
+  } else {
+    return dh;
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// LDS access helpers (byte offsets into dynamic shared memory, which starts at 0).
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 lds_read16(unsigned byte_off) {
+  return *(const FMLP_LDS u32x4*)(byte_off);
+}
+__device__ __forceinline__ u32x2 lds_read8(unsigned byte_off) {
+  return *(const FMLP_LDS u32x2*)(byte_off);
+}
+__device__ __forceinline__ u32x2 lds_read_tr(unsigned byte_off) {
+  i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLP_LDS i16x4*)(byte_off));
+  return __builtin_bit_cast(u32x2, r);
+}
+__device__ __forceinline__ void lds_write16(unsigned byte_off, const u32x4& v) {
+  *(FMLP_LDS u32x4*)(byte_off) = v;
+}
+__device__ __forceinline__ void lds_write8(unsigned byte_off, const u32x2& v) {
+  *(FMLP_LDS u32x2*)(byte_off) = v;
+}
+__device__ __forceinline__ u32x4 cat(const u32x2& lo, const u32x2& hi) {
+  u32x4 r = {lo[0], lo[1], hi[0], hi[1]};
+  return r;
+}
+
+// Row swizzle for row-major tiles whose rows are D 16-bit values (D = 64 or 128) and that
+// are read both row-wise (16-byte chunks, lane m reads row m) and with ds_read_b64_tr_b16
+// over 4-row x 32-byte blocks. 16-byte chunk c of row r is stored at chunk c ^ swz(r).
+// With 64 LDS banks x 4 B both patterns are conflict free (measured on MI355X).
+template <int D>
+__device__ __forceinline__ unsigned swz16(unsigned r) {
+  if constexpr (D == 128) return ((r & 3u) << 2) | ((r >> 2) & 3u);
+  else return (((r >> 1) & 1u) << 2) | ((r >> 2) & 3u);
+}
+// byte offset of (row r, column d) inside a [rows][D] tile with the 16-byte swizzle;
+// d must be a multiple of 4 (8-byte granularity).
+template <int D>
+__device__ __forceinline__ unsigned tile_off(unsigned r, unsigned d) {
+  unsigned c = d >> 3;
+  return r * (D * 2) + ((c ^ swz16<D>(r)) << 4) + ((d & 4u) << 1);
+}
+
+// W1 chunk tile [D rows][32 columns] (64-byte rows), read with ds_read_b64_tr_b16 over
+// 4 consecutive rows and with ds_read_b64 down 32 consecutive rows. 8-byte unit u of row r
+// is stored at unit u ^ ((r >> 2) & 7): conflict free for both patterns.
+__device__ __forceinline__ unsigned w1c_off(unsigned r, unsigned unit) {
+  return r * 64u + ((unit ^ ((r >> 2) & 7u)) << 3);
+}
+
+// ---------------------------------------------------------------------------------
+// Workgroup -> tile remap. Workgroups are dispatched round-robin over the 8 XCDs
+// (each with its own L2); this gives every XCD a contiguous range of logical tiles, so
+// tiles of the same head (which share weights / activations) run on the same L2.
+// Bijective on [0, n).
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  const int q = n >> 3, r = n & 7;
+  const int x = bid & 7, j = bid >> 3;
+  return x * q + (x < r ? x : r) + j;
+}
+
+}  // namespace fmlp

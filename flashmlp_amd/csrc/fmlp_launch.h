@@ -1,0 +1,51 @@
+// Host-side launch descriptors shared by the C-ABI layer and the kernel translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace fmlp {
+
+struct FwdArgs {
+  const void* x;
+  const void* w1;
+  const void* w2;
+  void* o;
+  int64_t H, B, D, E;
+  bool bf16;
+  int act;
+};
+
+// Backward work decomposition (chosen on the host, see plan_bwd):
+//   dW programs: H * nE * nS, each owning an E-tile of 128 columns and a B-range of
+//                rows_per_split rows (nS > 1 writes fp32 partials to the workspace).
+//   dX programs: H * dx_tiles_per_head, each owning dx_rows rows.
+struct BwdPlan {
+  int nE;              // E-tiles of 128 per head
+  int nS;              // B splits for the dW programs
+  int rows_per_split;  // multiple of 32
+  int dx_mt;           // 32-row M-tiles per wave in dX programs (rows per program = 128 * dx_mt)
+  int dx_tiles_per_head;
+  long long n_dw, n_dx;
+  size_t ws_bytes;     // fp32 partials when nS > 1
+};
+
+struct BwdArgs {
+  const void* x;
+  const void* w1;
+  const void* w2;
+  const void* dout;
+  void* dx;
+  void* dw1;
+  void* dw2;
+  int64_t H, B, D, E;
+  bool bf16;
+  int act;
+  void* ws;
+};
+
+BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus);
+hipError_t launch_fwd(const FwdArgs& a, hipStream_t st);
+hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st);
+
+}  // namespace fmlp

@@ -1,0 +1,202 @@
+"""FlashMLP Python API on MI355X: the reference's interface over the gfx950 HIP library.
+
+Same names, arguments, shapes and assertion messages as the reference module
+(flashmlp.py:428-616):
+
+    flashmlp_fwd(x, w1, w2, activation="") -> o                       (H,B,D)
+    flashmlp_bwd(x, w1, w2, do, activation="") -> (dx, dw1, dw2)      (H,B,D),(H,D,E),(H,E,D)
+    FlashMLPFunction.apply(x, w1, w2, activation)
+    FlashMLP(num_heads, hidden_dim, intermediate_dim, activation="silu",
+             dtype=torch.float16, device="cuda")
+
+O = act(X W1) W2 per head with act in {"", "silu", "leaky_relu", "sigmoid"}; an unknown
+activation string means linear, as in the reference. Every call launches the HIP kernels
+of libflashmlp.so asynchronously on torch's current stream of the tensors' device; there
+is no other execution path.
+
+Differences from the reference, all deliberate:
+  * outputs are allocated with torch.empty (the kernels overwrite every element) instead of
+    torch.zeros_like (flashmlp.py:462,516-518);
+  * flashmlp_bwd also checks the head counts (flashmlp.py:496-499 omits them);
+  * Leaky ReLU's derivative at Z == 0 is autograd's 0.01 (flashmlp.py:33-34 uses 1.0);
+  * io dtypes are fp16 and bf16; other dtypes raise TypeError.
+"""
+from __future__ import annotations
+
+from typing import Tuple
+
+import numpy as np
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.float16: _lib.FMLP_DTYPE_F16, torch.bfloat16: _lib.FMLP_DTYPE_BF16}
+
+
+def _act_code(activation: str) -> int:
+    return _lib.ACT_CODES.get(activation, 0)
+
+
+def _check_tensors(*ts: torch.Tensor) -> int:
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            f"FlashMLP runs on an AMD GPU through HIP; got a tensor on {dev} (move inputs to 'cuda')")
+    dt = ts[0].dtype
+    if dt not in _DTYPES:
+        raise TypeError(f"FlashMLP supports float16 and bfloat16 inputs, got {dt}")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"all tensors must be on one device ({dev} vs {t.device})")
+        if t.dtype != dt:
+            raise TypeError(f"all tensors must share one dtype ({dt} vs {t.dtype})")
+    return _DTYPES[dt]
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    # the kernels use 16-byte vector accesses; a view at an odd storage offset is copied
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation: str = "") -> torch.Tensor:
+    """FlashMLP forward pass (reference: flashmlp.py:428-477).
+
+    Args:
+        x: (H, B, D); w1: (H, D, E); w2: (H, E, D); activation: "silu", "leaky_relu",
+        "sigmoid" or "" (linear).
+    Returns:
+        O = act(x @ w1) @ w2 of shape (H, B, D), dtype of x.
+    """
+    assert x.shape[0] == w1.shape[0], "Number of heads must match"
+    assert x.shape[0] == w2.shape[0], "Number of heads must match"
+    assert x.shape[2] == w1.shape[1], "Hidden dimension mismatch"
+    assert w1.shape[2] == w2.shape[1], "Intermediate dimension mismatch"
+    assert x.shape[2] == w2.shape[2], "Output dimension mismatch"
+
+    H, B, D = x.shape
+    E = w1.shape[2]
+
+    x = x.reshape(H * B, D)
+    w1 = w1.reshape(D * H, E)
+    w2 = w2.reshape(E * H, D)
+
+    assert x.is_contiguous(), "Input X must be contiguous"
+    assert w1.is_contiguous(), "Weight W1 must be contiguous"
+    assert w2.is_contiguous(), "Weight W2 must be contiguous"
+
+    dtype = _check_tensors(x, w1, w2)
+    x, w1, w2 = _aligned(x), _aligned(w1), _aligned(w2)
+    o = torch.empty_like(x)
+    L = _lib.lib()
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        st = L.fmlp_fwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), o.data_ptr(), H, B, D, E, dtype,
+                        _act_code(activation), stream)
+    _lib.check(st, "forward")
+    return o.reshape(H, B, D)
+
+
+def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.Tensor,
+                 activation: str = "") -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """FlashMLP backward pass (reference: flashmlp.py:480-538).
+
+    Recomputes Z = x @ w1 and h = act(Z) instead of reading stored activations.
+    Returns (dx, dw1, dw2) shaped like (x, w1, w2).
+    """
+    assert x.shape[0] == w1.shape[0], "Number of heads must match"
+    assert x.shape[0] == w2.shape[0], "Number of heads must match"
+    assert x.shape[2] == w1.shape[1], "Hidden dimension mismatch"
+    assert w1.shape[2] == w2.shape[1], "Intermediate dimension mismatch"
+    assert x.shape[2] == w2.shape[2], "Output dimension mismatch"
+    assert x.shape == do.shape, "Gradient shape mismatch"
+
+    H, B, D = x.shape
+    E = w1.shape[2]
+
+    x = x.reshape(H * B, D)
+    w1 = w1.reshape(D * H, E)
+    w2 = w2.reshape(E * H, D)
+    do = do.reshape(H * B, D).contiguous()
+
+    assert x.is_contiguous(), "Input X must be contiguous"
+    assert w1.is_contiguous(), "Weight W1 must be contiguous"
+    assert w2.is_contiguous(), "Weight W2 must be contiguous"
+    assert do.is_contiguous(), "Gradient dO must be contiguous"
+
+    dtype = _check_tensors(x, w1, w2, do)
+    x, w1, w2, do = _aligned(x), _aligned(w1), _aligned(w2), _aligned(do)
+    dx = torch.empty_like(x)
+    dw1 = torch.empty_like(w1)
+    dw2 = torch.empty_like(w2)
+    L = _lib.lib()
+    with torch.cuda.device(x.device):
+        ws_bytes = int(L.fmlp_bwd_workspace_bytes(H, B, D, E, dtype))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        st = L.fmlp_bwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(), dw1.data_ptr(),
+                        dw2.data_ptr(), H, B, D, E, dtype, _act_code(activation),
+                        ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    _lib.check(st, "backward")
+    return dx.reshape(H, B, D), dw1.reshape(H, D, E), dw2.reshape(H, E, D)
+
+
+class FlashMLPFunction(torch.autograd.Function):
+    """Autograd binding (reference: flashmlp.py:545-557). Saves only (x, w1, w2)."""
+
+    @staticmethod
+    def forward(ctx, x, w1, w2, activation=""):
+        o = flashmlp_fwd(x, w1, w2, activation)
+        ctx.save_for_backward(x, w1, w2)
+        ctx.activation = activation
+        return o
+
+    @staticmethod
+    def backward(ctx, do):
+        x, w1, w2 = ctx.saved_tensors
+        dx, dw1, dw2 = flashmlp_bwd(x, w1, w2, do, ctx.activation)
+        return dx, dw1, dw2, None
+
+
+class FlashMLP(torch.nn.Module):
+    """Multi-head MLP module on the FlashMLP kernels (reference: flashmlp.py:564-616).
+
+    Args:
+        num_heads: number of heads H
+        hidden_dim: hidden dimension D
+        intermediate_dim: intermediate dimension E
+        activation: "silu", "leaky_relu", "sigmoid" or ""
+        dtype: weight dtype (float16 or bfloat16)
+        device: device of the weights
+
+    Parameters w1 (H, D, E) ~ randn / sqrt(E) and w2 (H, E, D) ~ randn / sqrt(D), as in
+    the reference (flashmlp.py:586-591). A 2-D input (B, D) is expanded to every head and
+    the output is the mean over heads (flashmlp.py:603-614).
+    """
+
+    def __init__(self, num_heads: int, hidden_dim: int, intermediate_dim: int,
+                 activation: str = "silu", dtype=torch.float16, device="cuda"):
+        super().__init__()
+        self.num_heads = num_heads
+        self.hidden_dim = hidden_dim
+        self.intermediate_dim = intermediate_dim
+        self.activation = activation
+
+        self.w1 = torch.nn.Parameter(
+            torch.randn(num_heads, hidden_dim, intermediate_dim, dtype=dtype, device=device) / np.sqrt(intermediate_dim)
+        )
+        self.w2 = torch.nn.Parameter(
+            torch.randn(num_heads, intermediate_dim, hidden_dim, dtype=dtype, device=device) / np.sqrt(hidden_dim)
+        )
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if x.dim() == 2:
+            x = x.unsqueeze(0).expand(self.num_heads, -1, -1)
+            squeeze_output = True
+        else:
+            squeeze_output = False
+
+        o = FlashMLPFunction.apply(x, self.w1, self.w2, self.activation)
+
+        if squeeze_output:
+            o = o.mean(dim=0)
+        return o

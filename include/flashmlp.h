@@ -1,0 +1,87 @@
+/*
+ * flashmlp.h — C ABI of the MI355X-native FlashMLP library (libflashmlp.so).
+ *
+ * The fused multi-head MLP  O = act(X W1) W2  per head, and its gradients, on gfx950
+ * (MI355X) with hand-written HIP kernels. This is the boundary under the Python API
+ * (flashmlp_fwd / flashmlp_bwd / FlashMLPFunction / FlashMLP); nothing else calls it.
+ *
+ * Layouts are the reference's (flashmlp.py:1-14, :453-455, :505-508): contiguous row-major
+ *   X, O, dO, dX : (H, B, D)      W1, dW1 : (H, D, E)      W2, dW2 : (H, E, D)
+ * Element type of every tensor is the io dtype (fp16 or bf16). All pointers are device
+ * pointers on the current HIP device, 16-byte aligned. The library never allocates: the
+ * caller passes every buffer, including the backward workspace.
+ *
+ * Calls are asynchronous on the given hipStream_t (NULL = default stream), never
+ * synchronise, keep no mutable global state and are reentrant. A non-zero return is one
+ * of fmlp_status; fmlp_status_string() names it and fmlp_last_error() (thread-local) says
+ * which argument was rejected.
+ */
+#ifndef FLASHMLP_H_
+#define FLASHMLP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FMLP_ABI_VERSION 1
+
+typedef enum {
+  FMLP_OK = 0,
+  FMLP_ERR_INVALID_ARG = 1, /* shape, pointer, alignment or size out of contract */
+  FMLP_ERR_UNSUPPORTED = 2, /* valid but not implemented (dtype, D, E % 8 != 0) */
+  FMLP_ERR_HIP = 3,         /* the HIP runtime reported an error */
+  FMLP_ERR_WORKSPACE = 4    /* workspace smaller than fmlp_bwd_workspace_bytes() */
+} fmlp_status;
+
+typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1 } fmlp_dtype;
+
+/* Activation codes; names as in the reference ("", "silu", "leaky_relu", "sigmoid"). */
+typedef enum { FMLP_ACT_NONE = 0, FMLP_ACT_SILU = 1, FMLP_ACT_LEAKY_RELU = 2, FMLP_ACT_SIGMOID = 3 } fmlp_act;
+
+/* ABI version of the loaded library (FMLP_ABI_VERSION it was built with). */
+int fmlp_abi_version(void);
+
+/* Static description of a status code. */
+const char* fmlp_status_string(int status);
+
+/* Detail of the last failing call on this thread ("" if none). */
+const char* fmlp_last_error(void);
+
+/* Activation code for a reference activation string. Unknown strings map to
+ * FMLP_ACT_NONE, like the reference's if/elif chain (flashmlp.py:140-147). */
+int fmlp_act_from_name(const char* name);
+
+/* Shapes the kernels support: 1 on success. D in {64, 128}; E % 8 == 0; H, B, E >= 1. */
+int fmlp_shape_supported(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
+
+/*
+ * Forward: o = act(x @ w1) @ w2 per head, fp32 accumulation, act(.) rounded to the io
+ * dtype before the second product. Replaces flashmlp_fwd's kernel launch
+ * (flashmlp.py:428-477, kernel flashmlp.py:63-158). o is fully overwritten.
+ */
+int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
+             int64_t E, int dtype, int act, void* stream);
+
+/* Bytes of device workspace fmlp_bwd needs for these shapes on the current device
+ * (0 when none is needed). */
+size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
+
+/*
+ * Backward: dx = dZ @ w1^T, dw1 = x^T @ dZ, dw2 = h^T @ dout with h = act(x @ w1),
+ * dZ = (dout @ w2^T) * act'(x @ w1); Z and h are recomputed, never stored. Replaces
+ * flashmlp_bwd's kernel launch (flashmlp.py:480-538, kernel flashmlp.py:341-421).
+ * dx, dw1, dw2 are fully overwritten. `workspace` may be NULL when
+ * fmlp_bwd_workspace_bytes() is 0.
+ */
+int fmlp_bwd(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1, void* dw2,
+             int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, void* workspace,
+             size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASHMLP_H_ */
