@@ -7,10 +7,17 @@
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <string>
 
 #define FMLP_EXPORT extern "C" __attribute__((visibility("default")))
+
+int fmlp::env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  if (v == nullptr || *v == 0) return dflt;
+  return std::atoi(v);
+}
 
 namespace {
 

@@ -22,19 +22,22 @@
 
 namespace fmlp {
 
-template <bool BF16, int D, int ACT, int NW, int MT>
-__global__ void __launch_bounds__(NW * 64)
+// LDS tiles (64-byte rows, no swizzle: every access below is a 4-row x 64-byte block per
+// 32-lane phase, which covers all 64 banks once):
+//   W1c  [D][32]           row d = W1[h][d][32c .. 32c+31]
+//   W2c  [D/32][32][32]    block nt, row e = W2[h][32c + e][32nt .. 32nt+31]
+template <bool BF16, int D, int ACT>
+__global__ void __launch_bounds__(256)
 fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            u16* __restrict__ O, int B, int E, int tiles_per_head) {
-  constexpr int NT = NW * 64;          // threads
-  constexpr int KS = D / 16;           // K steps of GEMM1
+  constexpr int NW = 4, NT = NW * 64;  // waves, threads
+  constexpr int KS = D / 16;           // K steps of GEMM1 (= GEMM2 operand count 2 * D/32)
   constexpr int NTN = D / 32;          // N tiles of GEMM2
-  constexpr int BB = NW * MT * 32;     // rows per workgroup
+  constexpr int BB = NW * 32;          // rows per workgroup (32 per wave)
   constexpr unsigned SLOT = 128u * D;  // bytes per ring slot: W1c (64*D) + W2c (64*D)
   constexpr unsigned W2OFF = 64u * D;
-  constexpr int NP = 8 * D;            // 16-byte pieces per chunk (half W1c, half W2c)
-  constexpr int PPT = NP / NT;         // first PPT/2 pieces of a thread are W1c, the rest W2c
-  static_assert(NP % (2 * NT) == 0, "pieces per thread");
+  constexpr int PPT = 8 * D / NT;      // 16-byte pieces per thread per chunk (half W1c, half W2c)
+  static_assert(PPT % 2 == 0, "pieces per thread");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
@@ -46,24 +49,23 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const u16* W1h = W1 + (size_t)h * D * E;
   const u16* W2h = W2 + (size_t)h * E * D;
   u16* Oh = O + (size_t)h * B * D;
-  const int b_wave = bt * BB + wave * MT * 32;
+  const int b_wave = bt * BB + wave * 32;
 
-  // ---- global -> register staging of one chunk, then register -> LDS ----
+  // ---- chunk staging: global -> registers (one chunk ahead) -> LDS ----
   u32x4 stg[PPT];
   auto load_chunk = [&](int c) {
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (k < PPT / 2) {  // W1c piece: row d, 8 columns at 8q
-        const int p = tid + k * NT;
+      const int p = tid + (k % (PPT / 2)) * NT;
+      if (k < PPT / 2) {  // W1c: row d, 16-byte piece q
         const int d = p >> 2, q = p & 3;
         const int e = c * 32 + q * 8;
         if (e < E) v = *(const u32x4*)(W1h + (size_t)d * E + e);
-      } else {            // W2c piece: row er, 8 columns at 8q
-        const int p = tid + (k - PPT / 2) * NT;
-        const int er = p / (D / 8), q = p % (D / 8);
+      } else {            // W2c: block nt, row er, 16-byte piece q
+        const int q = p & 3, er = (p >> 2) & 31, nt = p >> 7;
         const int e = c * 32 + er;
-        if (e < E) v = *(const u32x4*)(W2h + (size_t)e * D + q * 8);
+        if (e < E) v = *(const u32x4*)(W2h + (size_t)e * D + nt * 32 + q * 8);
       }
       stg[k] = v;
     }
@@ -72,166 +74,166 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     const unsigned base = slot * SLOT;
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
-      if (k < PPT / 2) {
-        const int p = tid + k * NT;
-        const int d = p >> 2, q = p & 3;
-        u32x2 lo = {stg[k][0], stg[k][1]}, hi = {stg[k][2], stg[k][3]};
-        lds_write8(base + w1c_off(d, 2 * q), lo);
-        lds_write8(base + w1c_off(d, 2 * q + 1), hi);
-      } else {
-        const int p = tid + (k - PPT / 2) * NT;
-        const int er = p / (D / 8), q = p % (D / 8);
-        lds_write16(base + W2OFF + tile_off<D>(er, q * 8), stg[k]);
-      }
+      const unsigned p = tid + (k % (PPT / 2)) * NT;
+      if (k < PPT / 2) lds_write16(base + p * 16u, stg[k]);  // d*64 + q*16
+      else lds_write16(base + W2OFF + (p >> 7) * 2048u + ((p >> 2) & 31u) * 64u + (p & 3u) * 16u, stg[k]);
     }
   };
 
-  // ---- X rows -> registers (B operand of Z^T = W1c^T X^T) ----
-  u32x4 xr[MT][KS];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int b = b_wave + mt * 32 + l32;
+  // ---- X rows -> registers (B operand of Z^T = W1c^T X^T: lane = row b, 8 consecutive d) ----
+  u32x4 xr[KS];
+  {
+    const int b = b_wave + l32;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (b < B) v = *(const u32x4*)(Xh + (size_t)b * D + ks * 16 + g * 8);
-      xr[mt][ks] = v;
+      xr[ks] = v;
     }
   }
 
-  // per-lane LDS offsets (slot-relative)
-  // GEMM1 A operand (tr read of W1c): rows 16ks + 8g + 4r + i16/4, unit 4(G%2) + i16%4
-  unsigned offA[2][2];
-#pragma unroll
-  for (int kp = 0; kp < 2; ++kp)
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-      offA[kp][r] = w1c_off(16 * kp + 8 * g + 4 * r + (i16 >> 2), 4 * (G & 1) + (i16 & 3));
-  // GEMM2 B operand (tr read of W2c): rows 16s + 8r + 4g + i16/4, column 32nt + 16(G%2) + 4(i16%4)
-  unsigned offB[2][2][NTN];
-#pragma unroll
-  for (int s = 0; s < 2; ++s)
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int nt = 0; nt < NTN; ++nt)
-        offB[s][r][nt] = W2OFF + tile_off<D>(16 * s + 8 * r + 4 * g + (i16 >> 2), 32 * nt + 16 * (G & 1) + 4 * (i16 & 3));
-
-  auto gemm1 = [&](int slot, f32x16 (&z)[MT]) {
-    const unsigned base = slot * SLOT;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) z[mt] = zero16();
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      // rows advance by 16 per ks: 16 rows * 64 B; the unit swizzle repeats every 32 rows
-      const unsigned a0 = base + offA[ks & 1][0] + (ks >> 1) * 2048u;
-      const unsigned a1 = base + offA[ks & 1][1] + (ks >> 1) * 2048u;
-      const u32x4 A = cat(lds_read_tr(a0), lds_read_tr(a1));
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) z[mt] = mfma<BF16>(A, xr[mt][ks], z[mt]);
-    }
+  // lane part of the transposed-read addresses (16-lane group G reads a 4x16 block; lane i16
+  // reads row i16/4, columns 4*(i16%4)..+3)
+  //   GEMM1 A (W1c^T): rows 16ks + 8g + 4r + i16/4, columns 16(G%2) + 4(i16%4)
+  //   GEMM2 B (W2c):   block nt, rows 16s + 8r + 4g + i16/4, columns 16(G%2) + 4(i16%4)
+  const unsigned laneA = (8 * g + (i16 >> 2)) * 64 + 32 * (G & 1) + 8 * (i16 & 3);
+  const unsigned laneB = W2OFF + (4 * g + (i16 >> 2)) * 64 + 32 * (G & 1) + 8 * (i16 & 3);
+  auto opndA = [&](unsigned base, int ks) {
+    return cat(lds_read_tr(base + laneA + ks * 1024u), lds_read_tr(base + laneA + ks * 1024u + 256u));
   };
-  f32x16 o[MT][NTN];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NTN; ++nt) o[mt][nt] = zero16();
-  auto gemm2 = [&](int slot, const u32x4 (&hA)[MT][2]) {
-    const unsigned base = slot * SLOT;
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) {
-        const u32x4 Bv = cat(lds_read_tr(base + offB[s][0][nt]), lds_read_tr(base + offB[s][1][nt]));
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) o[mt][nt] = mfma<BF16>(hA[mt][s], Bv, o[mt][nt]);
-      }
-  };
-  auto activate = [&](const f32x16 (&z)[MT], u32x4 (&hA)[MT][2]) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-          hA[mt][s][w] = pack2<BF16>(act_f<ACT>(z[mt][8 * s + 2 * w]), act_f<ACT>(z[mt][8 * s + 2 * w + 1]));
+  auto opndB = [&](unsigned base, int s, int nt) {
+    const unsigned a = base + laneB + nt * 2048u + s * 1024u;
+    return cat(lds_read_tr(a), lds_read_tr(a + 512u));
   };
 
-  // ---- prologue ----
+  f32x16 o[NTN];
+#pragma unroll
+  for (int nt = 0; nt < NTN; ++nt) o[nt] = zero16();
+
+  // ---- prologue: chunks 0 and 1 in LDS, chunk 2 in registers, Z^T(0) ----
   load_chunk(0);
   store_chunk(0);
   if (NC > 1) {
     load_chunk(1);
     store_chunk(1);
   }
+  load_chunk(NC > 2 ? 2 : NC - 1);
   __syncthreads();
-  f32x16 zc[MT];
-  gemm1(0, zc);
-  u32x4 hp[MT][2];
+  f32x16 zc = zero16();
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) zc = mfma<BF16>(opndA(0, ks), xr[ks], zc);
+  u32x4 hp, hc;  // h of the previous / current chunk, A operand of O += h W2c (two K steps)
+  u32x4 hp1, hc1;
 
-  // iteration body; G1: compute Z^T(c+1), G2: accumulate h(c-1) W2c(c-1)
+  // Iteration c (G1: Z^T(c+1) = W1c(c+1)^T X^T, G2: O += h(c-1) W2c(c-1), act: h(c)).
+  // Written as a fixed sequence of steps: each step issues one MFMA, the operand reads of
+  // the MFMA two steps later and a share of the activation; sched_barrier keeps the order.
   auto iter = [&](auto G1, auto G2, int c) {
     constexpr bool DO_G1 = decltype(G1)::value;
     constexpr bool DO_G2 = decltype(G2)::value;
-    load_chunk(c + 2 < NC ? c + 2 : NC - 1);
-    f32x16 zn[MT];
-    if constexpr (DO_G1) gemm1((c + 1) & 3, zn);
-    if constexpr (DO_G2) gemm2((c - 1) & 3, hp);
-    activate(zc, hp);
-    store_chunk((c + 2) & 3);
-    __syncthreads();
-    if constexpr (DO_G1) {
+    constexpr int N1 = DO_G1 ? KS : 0, N2 = DO_G2 ? KS : 0, NOPS = N1 + N2;
+    constexpr int PER = 16 / NOPS;  // activation elements per step
+    const unsigned base1 = ((c + 1) & 3) * SLOT, base2 = ((c - 1) & 3) * SLOT;
+
+    store_chunk((c + 2) & 3);                  // chunk c+2 (loaded during iteration c-1)
+    load_chunk(c + 3 < NC ? c + 3 : NC - 1);   // chunk c+3 -> registers
+    __builtin_amdgcn_sched_barrier(0);
+
+    // op j -> (is_g1, index): G1 and G2 alternate when both are present
+    auto is_g1 = [&](int j) { return DO_G1 && (!DO_G2 || (j % 2 == 0)); };
+    auto idx = [&](int j) { return (DO_G1 && DO_G2) ? j / 2 : j; };
+    auto fetch = [&](int j) {
+      const int k = idx(j);
+      return is_g1(j) ? opndA(base1, k) : opndB(base2, k / NTN, k % NTN);
+    };
+    f32x16 zn = zero16();
+    u32x4 op0 = fetch(0), op1 = NOPS > 1 ? fetch(1) : op0, op2 = op0;
+    float hv[16];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) zc[mt] = zn[mt];
+    for (int j = 0; j < NOPS; ++j) {
+      const u32x4 cur = (j % 3 == 0) ? op0 : (j % 3 == 1) ? op1 : op2;
+      if (j + 2 < NOPS) {
+        const u32x4 nx = fetch(j + 2);
+        if ((j + 2) % 3 == 0) op0 = nx; else if ((j + 2) % 3 == 1) op1 = nx; else op2 = nx;
+      }
+      const int k = idx(j);
+      if (is_g1(j)) {
+        zn = mfma<BF16>(cur, xr[k], zn);
+      } else {
+        const int s = k / NTN, nt = k % NTN;
+        o[nt] = mfma<BF16>(s == 0 ? hp : hp1, cur, o[nt]);
+      }
+#pragma unroll
+      for (int q = 0; q < PER; ++q) {
+        const int e = j * PER + q;
+        hv[e] = act_f<ACT>(zc[e]);
+        if (e & 1) {
+          const unsigned pk = pack2<BF16>(hv[e - 1], hv[e]);
+          const int w = (e >> 1) & 3;
+          if (e < 8) hc[w] = pk; else hc1[w] = pk;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    __syncthreads();
+    hp = hc;
+    hp1 = hc1;
+    if constexpr (DO_G1) zc = zn;
   };
   if (NC == 1) {
-    activate(zc, hp);
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const unsigned pk = pack2<BF16>(act_f<ACT>(zc[e]), act_f<ACT>(zc[e + 1]));
+      if (e < 8) hp[e >> 1] = pk; else hp1[(e - 8) >> 1] = pk;
+    }
   } else {
     iter(std::true_type{}, std::false_type{}, 0);
     for (int c = 1; c < NC - 1; ++c) iter(std::true_type{}, std::true_type{}, c);
     iter(std::false_type{}, std::true_type{}, NC - 1);
   }
-  gemm2((NC - 1) & 3, hp);
+  {
+    const unsigned base2 = ((NC - 1) & 3) * SLOT;
+#pragma unroll
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) o[nt] = mfma<BF16>(s == 0 ? hp : hp1, opndB(base2, s, nt), o[nt]);
+  }
 
   // ---- epilogue: O tile (C layout: lane = column d, rows 8(i/4) + 4g + i%4) ----
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int i = 0; i < 16; ++i) {
+    const int b = b_wave + 8 * (i >> 2) + 4 * g + (i & 3);
+    if (b < B) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int b = b_wave + mt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-      if (b < B) {
-#pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) Oh[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(o[mt][nt][i]);
-      }
+      for (int nt = 0; nt < NTN; ++nt) Oh[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(o[nt][i]);
     }
+  }
 }
 
 // ------------------------------------------------------------------------------------
 // launcher
 // ------------------------------------------------------------------------------------
-template <bool BF16, int D, int ACT, int NW, int MT>
+template <bool BF16, int D, int ACT>
 static hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t st) {
-  constexpr int BB = NW * MT * 32;
+  constexpr int BB = 128;
   const int tiles_per_head = (int)((a.B + BB - 1) / BB);
   const long long grid = (long long)tiles_per_head * a.H;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   const size_t lds = 4u * 128u * D;
-  auto k = fwd_kernel<BF16, D, ACT, NW, MT>;
+  auto k = fwd_kernel<BF16, D, ACT>;
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(NW * 64), lds, st, (const u16*)a.x, (const u16*)a.w1,
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(256), lds, st, (const u16*)a.x, (const u16*)a.w1,
                      (const u16*)a.w2, (u16*)a.o, (int)a.B, (int)a.E, tiles_per_head);
   return hipGetLastError();
 }
 
 template <bool BF16, int D, int ACT>
 static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t st) {
-  // Tile choice: 4 waves x 64 rows when the grid still covers the chip, else 32 rows.
-  const long long big_tiles = ((a.B + 255) / 256) * a.H;
-  if (big_tiles >= 2 * 256) return launch_fwd_t<BF16, D, ACT, 4, 2>(a, st);
-  return launch_fwd_t<BF16, D, ACT, 4, 1>(a, st);
+  // 4 waves x 32 rows per workgroup; two workgroups share a CU (two waves per SIMD)
+  return launch_fwd_t<BF16, D, ACT>(a, st);
 }
 
 template <bool BF16, int D>

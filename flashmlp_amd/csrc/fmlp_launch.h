@@ -6,6 +6,9 @@
 
 namespace fmlp {
 
+// Integer tuning override from the environment (tile shapes); `dflt` when unset.
+int env_int(const char* name, int dflt);
+
 struct FwdArgs {
   const void* x;
   const void* w1;
