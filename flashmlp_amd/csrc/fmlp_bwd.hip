@@ -176,20 +176,71 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
       load_sub(1);
       store_sub(1);
     }
+    load_sub(nsub > 2 ? 2 : nsub - 1);
     __syncthreads();
     f32x16 zc, dhc;
     gemm_zh(0, zc, dhc);
     u32x4 hp[2], dzp[2];
+    // Iteration k: recompute Z, dH of subtile k+1 (group 1), accumulate dW over subtile
+    // k-1 (group 2) and activate subtile k, as a fixed sequence of steps: one MFMA each,
+    // operand reads PD steps ahead, activation spread over the steps.
     auto iter = [&](auto G1, auto G2, int k) {
       constexpr bool DO_G1 = decltype(G1)::value;
       constexpr bool DO_G2 = decltype(G2)::value;
-      load_sub(k + 2 < nsub ? k + 2 : nsub - 1);
-      f32x16 zn, dhn;
-      if constexpr (DO_G1) gemm_zh((k + 1) & 3, zn, dhn);
-      if constexpr (DO_G2) gemm_dw((k - 1) & 3, hp, dzp);
-      activate(zc, dhc, hp, dzp);
-      store_sub((k + 2) & 3);
+      constexpr int N1 = DO_G1 ? 2 * KS : 0, N2 = DO_G2 ? 4 * NTN : 0, NOPS = N1 + N2;
+      constexpr int PD = 3;
+      const unsigned base1 = ((k + 1) & 3) * SLOT, base2 = ((k - 1) & 3) * SLOT;
+      store_sub((k + 2) & 3);                    // subtile k+2 (loaded during iteration k-1)
+      load_sub(k + 3 < nsub ? k + 3 : nsub - 1);  // subtile k+3 -> registers
+      __builtin_amdgcn_sched_barrier(0);
+      auto fetch = [&](int j) -> u32x4 {
+        const int q = sched_index(j, N1, N2);
+        if (sched_is_g2(j, N1, N2)) {  // (s, nt, which): which 0 -> dW2 (B = dO^T), 1 -> dW1^T (B = X^T)
+          const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1, which = q & 1;
+          const unsigned b = base2 + (which == 0 ? DOOFF : 0u);
+          return cat(lds_read_tr(b + offTr[s2][0][nt]), lds_read_tr(b + offTr[s2][1][nt]));
+        }
+        const int ks = q >> 1, which = q & 1;  // which 0 -> Z (A = X), 1 -> dH (A = dO)
+        return lds_read16(base1 + (which ? DOOFF : 0u) + offRow[ks]);
+      };
+      f32x16 zn = zero16(), dhn = zero16();
+      u32x4 hc[2], dzc[2];
+      float hv[16], dv[16];
+      u32x4 ring[PD + 1];
+#pragma unroll
+      for (int j = 0; j < PD && j < NOPS; ++j) ring[j] = fetch(j);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = 0; j < NOPS; ++j) {
+        const u32x4 cur = ring[j % (PD + 1)];
+        if (j + PD < NOPS) ring[(j + PD) % (PD + 1)] = fetch(j + PD);
+        const int q = sched_index(j, N1, N2);
+        if (sched_is_g2(j, N1, N2)) {
+          const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1;
+          if ((q & 1) == 0) a2[nt] = mfma<BF16>(hp[s2], cur, a2[nt]);
+          else a1[nt] = mfma<BF16>(dzp[s2], cur, a1[nt]);
+        } else {
+          const int ks = q >> 1;
+          if ((q & 1) == 0) zn = mfma<BF16>(cur, w1t[ks], zn);
+          else dhn = mfma<BF16>(cur, w2r[ks], dhn);
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          if (sched_elem_at(e, j, NOPS, 16)) {
+            act_fb<ACT>(zc[e], dhc[e], hv[e], dv[e]);
+            if (e & 1) {
+              hc[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1], hv[e]);
+              dzc[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
+            }
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
       __syncthreads();
+      hp[0] = hc[0];
+      hp[1] = hc[1];
+      dzp[0] = dzc[0];
+      dzp[1] = dzc[1];
       if constexpr (DO_G1) {
         zc = zn;
         dhc = dhn;
@@ -394,23 +445,80 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
     load_chunk(1);
     store_chunk(1);
   }
+  load_chunk(NC > 2 ? 2 : NC - 1);
   __syncthreads();
   f32x16 zc[MT], dhc[MT];
   gemm_zh(0, zc, dhc);
   u32x4 dzp[MT][2];
+  // Iteration c: recompute Z^T, dH^T of chunk c+1 (group 1), accumulate dX over chunk c-1
+  // (group 2) and form dZ of chunk c, as a fixed sequence of steps (see the dW role).
   auto iter = [&](auto G1, auto G2, int c) {
     constexpr bool DO_G1 = decltype(G1)::value;
     constexpr bool DO_G2 = decltype(G2)::value;
-    load_chunk(c + 2 < NC ? c + 2 : NC - 1);
+    constexpr int N1 = DO_G1 ? 2 * KS : 0, N2 = DO_G2 ? 2 * NTN : 0, NOPS = N1 + N2;
+    constexpr int NEL = 16 * MT;
+    constexpr int PD = 3;
+    const unsigned base1 = ((c + 1) & 3) * SLOT, base2 = ((c - 1) & 3) * SLOT;
+    store_chunk((c + 2) & 3);                  // chunk c+2 (loaded during iteration c-1)
+    load_chunk(c + 3 < NC ? c + 3 : NC - 1);   // chunk c+3 -> registers
+    __builtin_amdgcn_sched_barrier(0);
+    auto fetch = [&](int j) -> u32x4 {
+      const int q = sched_index(j, N1, N2);
+      if (sched_is_g2(j, N1, N2)) {  // dX += dZ W1c^T: B = W1c rows (e-runs of 4)
+        const int s2 = q / NTN, nt = q % NTN;
+        return cat(lds_read8(base2 + offW1[s2][0][nt]), lds_read8(base2 + offW1[s2][1][nt]));
+      }
+      const int ks = q >> 1;
+      if ((q & 1) == 0)  // Z^T: A = W1c^T (transposed read)
+        return cat(lds_read_tr(base1 + offA[ks & 1][0] + (ks >> 1) * 2048u),
+                   lds_read_tr(base1 + offA[ks & 1][1] + (ks >> 1) * 2048u));
+      return lds_read16(base1 + offW2[ks]);  // dH^T: A = W2c rows
+    };
     f32x16 zn[MT], dhn[MT];
-    if constexpr (DO_G1) gemm_zh((c + 1) & 3, zn, dhn);
-    if constexpr (DO_G2) gemm_dx((c - 1) & 3, dzp);
-    activate(zc, dhc, dzp);
-    store_chunk((c + 2) & 3);
-    __syncthreads();
-    if constexpr (DO_G1) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
+    for (int mt = 0; mt < MT; ++mt) {
+      zn[mt] = zero16();
+      dhn[mt] = zero16();
+    }
+    u32x4 dzc[MT][2];
+    float dv[NEL];
+    u32x4 ring[PD + 1];
+#pragma unroll
+    for (int j = 0; j < PD && j < NOPS; ++j) ring[j] = fetch(j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NOPS; ++j) {
+      const u32x4 cur = ring[j % (PD + 1)];
+      if (j + PD < NOPS) ring[(j + PD) % (PD + 1)] = fetch(j + PD);
+      const int q = sched_index(j, N1, N2);
+      if (sched_is_g2(j, N1, N2)) {
+        const int s2 = q / NTN, nt = q % NTN;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma<BF16>(dzp[mt][s2], cur, acc[mt][nt]);
+      } else {
+        const int ks = q >> 1;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if ((q & 1) == 0) zn[mt] = mfma<BF16>(cur, xr[mt][ks], zn[mt]);
+          else dhn[mt] = mfma<BF16>(cur, dr[mt][ks], dhn[mt]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < NEL; ++e) {
+        if (sched_elem_at(e, j, NOPS, NEL)) {
+          const int mt = e >> 4, i = e & 15;
+          dv[e] = act_b<ACT>(zc[mt][i], dhc[mt][i]);
+          if (e & 1) dzc[mt][i >> 3][(i >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      dzp[mt][0] = dzc[mt][0];
+      dzp[mt][1] = dzc[mt][1];
+      if constexpr (DO_G1) {
         zc[mt] = zn[mt];
         dhc[mt] = dhn[mt];
       }

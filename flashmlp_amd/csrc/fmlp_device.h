@@ -189,6 +189,23 @@ __device__ __forceinline__ unsigned w1c_off(unsigned r, unsigned unit) {
 }
 
 // ---------------------------------------------------------------------------------
+// Step schedules. An iteration issues n1 MFMAs of one group and n2 of another; step j
+// issues exactly one of them, with the n2 group spread evenly (Bresenham) among the n1.
+// With the loops fully unrolled these fold to constants.
+// ---------------------------------------------------------------------------------
+__device__ __forceinline__ constexpr int sched_g2_before(int j, int n1, int n2) { return (j * n2) / (n1 + n2); }
+__device__ __forceinline__ constexpr bool sched_is_g2(int j, int n1, int n2) {
+  return sched_g2_before(j + 1, n1, n2) != sched_g2_before(j, n1, n2);
+}
+__device__ __forceinline__ constexpr int sched_index(int j, int n1, int n2) {
+  return sched_is_g2(j, n1, n2) ? sched_g2_before(j, n1, n2) : j - sched_g2_before(j, n1, n2);
+}
+// element e of an iteration's n_elem activations is computed at step (e * nsteps) / n_elem
+__device__ __forceinline__ constexpr bool sched_elem_at(int e, int j, int nsteps, int n_elem) {
+  return (e * nsteps) / n_elem == j;
+}
+
+// ---------------------------------------------------------------------------------
 // Workgroup -> tile remap. Workgroups are dispatched round-robin over the 8 XCDs
 // (each with its own L2); this gives every XCD a contiguous range of logical tiles, so
 // tiles of the same head (which share weights / activations) run on the same L2.
