@@ -1,0 +1,124 @@
+"""The C ABI library (libflashmlp.so) loads, exports every symbol include/flashmlp.h declares,
+and rejects out-of-contract arguments on the host, before any GPU work (runs without a GPU).
+"""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from flashmlp_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "flashmlp.h"
+
+OK, INVALID, UNSUPPORTED, HIPERR, WORKSPACE = 0, 1, 2, 3, 4
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fmlp_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libflashmlp.so not built (python -m flashmlp_amd.build)")
+    return _lib.lib()
+
+
+def test_header_declares_expected_entry_points():
+    names = declared_functions()
+    assert names == sorted(_lib.SIGNATURES), names
+
+
+def test_library_exports_every_declared_symbol(L):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    for name in declared_functions():
+        assert name in exported, name
+        assert getattr(L, name) is not None
+
+
+def test_version_and_status_strings(L):
+    assert L.fmlp_abi_version() == 1
+    assert L.fmlp_status_string(OK) == b"ok"
+    for st in (INVALID, UNSUPPORTED, HIPERR, WORKSPACE):
+        assert L.fmlp_status_string(st) not in (b"ok", b"unknown status")
+    assert L.fmlp_status_string(99) == b"unknown status"
+
+
+def test_activation_names_mirror_reference(L):
+    # flashmlp.py:140-147: unknown strings fall through to linear
+    assert L.fmlp_act_from_name(b"silu") == 1
+    assert L.fmlp_act_from_name(b"leaky_relu") == 2
+    assert L.fmlp_act_from_name(b"sigmoid") == 3
+    assert L.fmlp_act_from_name(b"") == 0
+    assert L.fmlp_act_from_name(b"gelu") == 0
+    assert L.fmlp_act_from_name(None) == 0
+
+
+def test_shape_support(L):
+    assert L.fmlp_shape_supported(32, 16384, 128, 1024, 1) == 1
+    assert L.fmlp_shape_supported(8, 4097, 64, 2048, 0) == 1
+    assert L.fmlp_shape_supported(1, 1, 64, 8, 1) == 1
+    assert L.fmlp_shape_supported(2, 8, 96, 64, 1) == 0   # D
+    assert L.fmlp_shape_supported(2, 8, 64, 12, 1) == 0   # E % 8
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 2) == 0   # dtype
+    assert L.fmlp_shape_supported(-1, 8, 64, 64, 1) == 0
+
+
+def _fwd(L, x=0x1000, w1=0x1000, w2=0x1000, o=0x1000, H=2, B=8, D=64, E=64, dtype=1, act=1):
+    return L.fmlp_fwd(x, w1, w2, o, H, B, D, E, dtype, act, None)
+
+
+def test_forward_argument_validation(L):
+    assert _fwd(L, D=96) == UNSUPPORTED
+    assert b"D=96" in L.fmlp_last_error()
+    assert _fwd(L, E=20) == UNSUPPORTED
+    assert _fwd(L, dtype=5) == UNSUPPORTED
+    assert _fwd(L, act=7) == INVALID
+    assert _fwd(L, H=-2) == INVALID
+    assert _fwd(L, x=None) == INVALID
+    assert b"x is NULL" in L.fmlp_last_error()
+    assert _fwd(L, w2=0x1008) == INVALID
+    assert b"aligned" in L.fmlp_last_error()
+    # nothing to do: no pointers needed, no GPU touched
+    assert _fwd(L, x=None, o=None, B=0) == OK
+    assert L.fmlp_last_error() == b""
+
+
+def test_backward_argument_validation(L):
+    p = 0x2000
+
+    def bwd(**kw):
+        a = dict(x=p, w1=p, w2=p, do=p, dx=p, dw1=p, dw2=p, H=2, B=8, D=128, E=64, dtype=1, act=2, ws=None, nws=0)
+        a.update(kw)
+        return L.fmlp_bwd(a["x"], a["w1"], a["w2"], a["do"], a["dx"], a["dw1"], a["dw2"], a["H"], a["B"], a["D"],
+                          a["E"], a["dtype"], a["act"], a["ws"], a["nws"], None)
+
+    assert bwd(D=32) == UNSUPPORTED
+    assert bwd(dw1=None) == INVALID
+    assert b"dw1" in L.fmlp_last_error()
+    assert bwd(do=0x2004) == INVALID
+    assert bwd(act=-1) == INVALID
+    assert bwd(H=0, x=None, do=None, dx=None) == OK
+
+
+def test_workspace_query_is_zero_for_invalid_shapes(L):
+    assert L.fmlp_bwd_workspace_bytes(2, 8, 96, 64, 1) == 0
+
+
+def test_last_error_is_thread_local(L):
+    import threading
+
+    assert _fwd(L, D=96) == UNSUPPORTED
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(L.fmlp_last_error()))
+    t.start()
+    t.join()
+    assert seen == [b""]
+    assert b"D=96" in L.fmlp_last_error()

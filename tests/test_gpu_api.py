@@ -1,0 +1,139 @@
+"""GPU behaviour of the Python API (FlashMLPFunction, FlashMLP, low-level functions) through
+the C ABI, against the CPU oracle; mirrors the reference's test_autograd / test_module
+(flashmlp.py:799-887) with real asserts."""
+import sys
+
+import pytest
+import torch
+
+import flashmlp_amd as fm
+from oracle import reference
+from oracle.inputs import make_inputs
+
+pytestmark = pytest.mark.gpu
+TOL = dict(atol=3e-2, rtol=3e-2)
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def test_autograd_matches_oracle():
+    # flashmlp.py:799-855 shape and activation, with N(0,1) / N(0,1/D) / N(0,1/E) inputs
+    _say("[api] autograd H=8 B=512 D=64 E=512 silu bf16")
+    x, w1, w2, do = make_inputs(8, 512, 64, 512, torch.bfloat16, seed=42)
+    xd, w1d, w2d = (t.cuda().requires_grad_(True) for t in (x, w1, w2))
+    o = fm.FlashMLPFunction.apply(xd, w1d, w2d, "silu")
+    o.backward(do.cuda())
+    ro, rdx, rdw1, rdw2 = reference.autograd_grads(x, w1, w2, do, "silu")
+    torch.testing.assert_close(o.detach().float().cpu(), ro, **TOL)
+    torch.testing.assert_close(xd.grad.float().cpu(), rdx, **TOL)
+    torch.testing.assert_close(w1d.grad.float().cpu(), rdw1, **TOL)
+    torch.testing.assert_close(w2d.grad.float().cpu(), rdw2, **TOL)
+
+
+def test_autograd_sum_loss_stride0_grad():
+    # o.sum().backward() hands the backward a stride-0 dO (flashmlp.py:508 makes it contiguous)
+    _say("[api] sum loss")
+    x, w1, w2, _ = make_inputs(4, 130, 128, 256, torch.bfloat16, seed=1)
+    xd, w1d, w2d = (t.cuda().requires_grad_(True) for t in (x, w1, w2))
+    fm.FlashMLPFunction.apply(xd, w1d, w2d, "leaky_relu").sum().backward()
+    ones = torch.ones(4, 130, 128)
+    _, rdx, rdw1, rdw2 = reference.autograd_grads(x, w1, w2, ones, "leaky_relu")
+    torch.testing.assert_close(xd.grad.float().cpu(), rdx, **TOL)
+    torch.testing.assert_close(w1d.grad.float().cpu(), rdw1, atol=3e-2, rtol=3e-2)
+    torch.testing.assert_close(w2d.grad.float().cpu(), rdw2, atol=3e-2, rtol=3e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_module_3d_and_2d_inputs(dtype):
+    # flashmlp.py:858-887 plus the 2-D path (expand to heads, mean over heads, :603-614)
+    _say(f"[api] module {dtype}")
+    torch.manual_seed(42)
+    m = fm.FlashMLP(num_heads=8, hidden_dim=64, intermediate_dim=512, activation="silu", dtype=dtype, device="cuda")
+    w1, w2 = m.w1.detach().float().cpu(), m.w2.detach().float().cpu()
+    x = torch.randn(8, 512, 64).to(dtype)
+    xd = x.cuda().requires_grad_(True)
+    o = m(xd)
+    assert o.shape == (8, 512, 64)
+    o.sum().backward()
+    assert xd.grad is not None and m.w1.grad is not None and m.w2.grad is not None
+    ro, rdx, _, _ = reference.autograd_grads(x, w1, w2, torch.ones(8, 512, 64), "silu")
+    torch.testing.assert_close(o.detach().float().cpu(), ro, **TOL)
+    torch.testing.assert_close(xd.grad.float().cpu(), rdx, **TOL)
+    # 2-D input
+    m.zero_grad()
+    x2 = torch.randn(300, 64).to(dtype)
+    x2d = x2.cuda().requires_grad_(True)
+    o2 = m(x2d)
+    assert o2.shape == (300, 64)
+    o2.sum().backward()
+    xe = x2.float().unsqueeze(0).expand(8, -1, -1).contiguous().requires_grad_(True)
+    ref = reference.torch_fwd(xe, w1, w2, "silu").mean(0)
+    ref.sum().backward()
+    torch.testing.assert_close(o2.detach().float().cpu(), ref.detach(), **TOL)
+    torch.testing.assert_close(x2d.grad.float().cpu(), xe.grad.sum(0), **TOL)
+
+
+def test_unsupported_dtype_and_device_errors():
+    x, w1, w2, _ = make_inputs(2, 8, 64, 64, torch.float32)
+    with pytest.raises(TypeError, match="float16 and bfloat16"):
+        fm.flashmlp_fwd(x.cuda(), w1.cuda(), w2.cuda(), "silu")
+    with pytest.raises(TypeError, match="one dtype"):
+        fm.flashmlp_fwd(x.cuda().bfloat16(), w1.cuda().half(), w2.cuda().bfloat16(), "silu")
+    with pytest.raises(RuntimeError, match="unsupported"):
+        xb = torch.zeros(2, 8, 96, dtype=torch.bfloat16, device="cuda")
+        fm.flashmlp_fwd(xb, torch.zeros(2, 96, 64, dtype=torch.bfloat16, device="cuda"),
+                        torch.zeros(2, 64, 96, dtype=torch.bfloat16, device="cuda"), "silu")
+
+
+def test_views_streams_and_unknown_activation():
+    _say("[api] views/streams")
+    x, w1, w2, do = make_inputs(3, 100, 64, 128, torch.bfloat16, seed=5)
+    ref_o = fm.flashmlp_fwd(x.cuda(), w1.cuda(), w2.cuda(), "")
+    # non-contiguous x: reshape copies, as in the reference
+    xt = x.transpose(0, 1).contiguous().cuda().transpose(0, 1)
+    assert not xt.is_contiguous()
+    torch.testing.assert_close(fm.flashmlp_fwd(xt, w1.cuda(), w2.cuda(), ""), ref_o, atol=0, rtol=0)
+    # a view at a 2-byte storage offset (not 16-byte aligned)
+    buf = torch.empty(x.numel() + 1, dtype=torch.bfloat16, device="cuda")
+    xv = buf[1:].view(x.shape)
+    xv.copy_(x.cuda())
+    torch.testing.assert_close(fm.flashmlp_fwd(xv, w1.cuda(), w2.cuda(), ""), ref_o, atol=0, rtol=0)
+    # unknown activation string means linear (flashmlp.py:146-147)
+    torch.testing.assert_close(fm.flashmlp_fwd(x.cuda(), w1.cuda(), w2.cuda(), "gelu"), ref_o, atol=0, rtol=0)
+    # a non-default stream
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        xs, w1s, w2s, dos = x.cuda(), w1.cuda(), w2.cuda(), do.cuda()
+        o_s = fm.flashmlp_fwd(xs, w1s, w2s, "")
+        g_s = fm.flashmlp_bwd(xs, w1s, w2s, dos, "")
+    s.synchronize()
+    torch.testing.assert_close(o_s, ref_o, atol=0, rtol=0)
+    g = fm.flashmlp_bwd(x.cuda(), w1.cuda(), w2.cuda(), do.cuda(), "")
+    for a, b in zip(g_s, g):
+        torch.testing.assert_close(a, b, atol=0, rtol=0)
+
+
+def test_empty_batch():
+    x = torch.zeros(2, 0, 64, dtype=torch.bfloat16, device="cuda")
+    _, w1, w2, _ = make_inputs(2, 1, 64, 64, torch.bfloat16)
+    w1, w2 = w1.cuda(), w2.cuda()
+    o = fm.flashmlp_fwd(x, w1, w2, "silu")
+    assert o.shape == (2, 0, 64)
+    dx, dw1, dw2 = fm.flashmlp_bwd(x, w1, w2, torch.zeros_like(x), "silu")
+    assert dx.shape == (2, 0, 64)
+    assert torch.count_nonzero(dw1) == 0 and torch.count_nonzero(dw2) == 0
+
+
+def test_leaky_relu_zero_point_follows_autograd():
+    # rows of X that are exactly zero give Z == 0: autograd's slope 0.01 applies there
+    # (the reference Triton kernel uses 1, flashmlp.py:33-34); dX differs by 100x
+    _say("[api] leaky zero rows")
+    x, w1, w2, do = make_inputs(16, 256, 128, 512, torch.bfloat16, seed=3)
+    x[:, ::7] = 0
+    dx, dw1, dw2 = fm.flashmlp_bwd(x.cuda(), w1.cuda(), w2.cuda(), do.cuda(), "leaky_relu")
+    _, rdx, rdw1, rdw2 = reference.autograd_grads(x, w1, w2, do, "leaky_relu")
+    torch.testing.assert_close(dx.float().cpu(), rdx, **TOL)
+    assert rdx[:, ::7].abs().max() > 0
