@@ -57,13 +57,18 @@ def make_gpu_inputs(H, B, D, E, dtype, x_std, seed=0):
 
 
 def traffic_from_profile(workload):
-    """HBM bytes per backward launch measured with rocprofv3 PMC counters (committed
-    summary), or None."""
-    path = os.path.join(ROOT, "profiles", f"bwd_kernel_{workload}_traffic.json")
+    """HBM bytes per backward launch from the committed rocprofv3 PMC summary
+    (FETCH_SIZE and WRITE_SIZE runs, each scaled by the same counter's reading for a
+    device copy of known size), or None when no summary exists for this workload."""
+    path = os.path.join(ROOT, "profiles", f"bwd_kernel_{workload}_traffic.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        for line in f:
+            key, _, val = line.partition("=")
+            if key.strip() == "hbm_bytes_per_launch_bwd":
+                return int(float(val))
+    return None
 
 
 def cpu_baseline(H, B, D, E, activation, x_std, budget_s=10.0):
