@@ -27,7 +27,7 @@ namespace fmlp {
 //   W1c  [D][32]           row d = W1[h][d][32c .. 32c+31]
 //   W2c  [D/32][32][32]    block nt, row e = W2[h][32c + e][32nt .. 32nt+31]
 template <bool BF16, int D, int ACT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            u16* __restrict__ O, int B, int E, int tiles_per_head) {
   constexpr int NW = 4, NT = NW * 64;  // waves, threads
@@ -119,16 +119,23 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   }
   load_chunk(NC > 2 ? 2 : NC - 1);
   __syncthreads();
-  f32x16 zc = zero16();
+  // Pipeline state carried between iterations: Z^T of the chunk to activate and h of the
+  // previous chunk (A operand of O += h W2c, two K steps). Iterations run in pairs with the
+  // two state copies swapping roles, so nothing is copied between iterations.
+  struct St {
+    f32x16 z;
+    u32x4 h0, h1;
+  };
+  St sa, sb;
+  sa.z = zero16();
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) zc = mfma<BF16>(opndA(0, ks), xr[ks], zc);
-  u32x4 hp, hc;  // h of the previous / current chunk, A operand of O += h W2c (two K steps)
-  u32x4 hp1, hc1;
+  for (int ks = 0; ks < KS; ++ks) sa.z = mfma<BF16>(opndA(0, ks), xr[ks], sa.z);
 
-  // Iteration c (G1: Z^T(c+1) = W1c(c+1)^T X^T, G2: O += h(c-1) W2c(c-1), act: h(c)).
-  // Written as a fixed sequence of steps: each step issues one MFMA, the operand reads of
-  // the MFMA two steps later and a share of the activation; sched_barrier keeps the order.
-  auto iter = [&](auto G1, auto G2, int c) {
+  // Iteration c (G1: Z^T(c+1) = W1c(c+1)^T X^T, G2: O += h(c-1) W2c(c-1), act: h(c)), reading
+  // `in` (Z^T(c), h(c-1)) and writing `out` (Z^T(c+1), h(c)). Written as a fixed sequence of
+  // steps: each step issues one MFMA, the operand reads of the MFMA two steps later and a
+  // share of the activation; sched_barrier keeps the order.
+  auto iter = [&](auto G1, auto G2, int c, St& in, St& out) {
     constexpr bool DO_G1 = decltype(G1)::value;
     constexpr bool DO_G2 = decltype(G2)::value;
     constexpr int N1 = DO_G1 ? KS : 0, N2 = DO_G2 ? KS : 0, NOPS = N1 + N2;
@@ -139,14 +146,14 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     load_chunk(c + 3 < NC ? c + 3 : NC - 1);   // chunk c+3 -> registers
     __builtin_amdgcn_sched_barrier(0);
 
-    // op j -> (is_g1, index): G1 and G2 alternate when both are present
+    // op j: G1 and G2 alternate when both are present
     auto is_g1 = [&](int j) { return DO_G1 && (!DO_G2 || (j % 2 == 0)); };
     auto idx = [&](int j) { return (DO_G1 && DO_G2) ? j / 2 : j; };
     auto fetch = [&](int j) {
       const int k = idx(j);
       return is_g1(j) ? opndA(base1, k) : opndB(base2, k / NTN, k % NTN);
     };
-    f32x16 zn = zero16();
+    if constexpr (DO_G1) out.z = zero16();
     u32x4 op0 = fetch(0), op1 = NOPS > 1 ? fetch(1) : op0, op2 = op0;
     float hv[16];
     __builtin_amdgcn_sched_barrier(0);
@@ -159,45 +166,56 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       }
       const int k = idx(j);
       if (is_g1(j)) {
-        zn = mfma<BF16>(cur, xr[k], zn);
+        out.z = mfma<BF16>(cur, xr[k], out.z);
       } else {
         const int s = k / NTN, nt = k % NTN;
-        o[nt] = mfma<BF16>(s == 0 ? hp : hp1, cur, o[nt]);
+        o[nt] = mfma<BF16>(s == 0 ? in.h0 : in.h1, cur, o[nt]);
       }
 #pragma unroll
       for (int q = 0; q < PER; ++q) {
         const int e = j * PER + q;
-        hv[e] = act_f<ACT>(zc[e]);
+        hv[e] = act_f<ACT>(in.z[e]);
         if (e & 1) {
           const unsigned pk = pack2<BF16>(hv[e - 1], hv[e]);
           const int w = (e >> 1) & 3;
-          if (e < 8) hc[w] = pk; else hc1[w] = pk;
+          if (e < 8) out.h0[w] = pk; else out.h1[w] = pk;
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
-    hp = hc;
-    hp1 = hc1;
-    if constexpr (DO_G1) zc = zn;
   };
-  if (NC == 1) {
-#pragma unroll
-    for (int e = 0; e < 16; e += 2) {
-      const unsigned pk = pack2<BF16>(act_f<ACT>(zc[e]), act_f<ACT>(zc[e + 1]));
-      if (e < 8) hp[e >> 1] = pk; else hp1[(e - 8) >> 1] = pk;
-    }
-  } else {
-    iter(std::true_type{}, std::false_type{}, 0);
-    for (int c = 1; c < NC - 1; ++c) iter(std::true_type{}, std::true_type{}, c);
-    iter(std::false_type{}, std::true_type{}, NC - 1);
-  }
-  {
+  auto last_gemm2 = [&](const St& st) {
     const unsigned base2 = ((NC - 1) & 3) * SLOT;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) o[nt] = mfma<BF16>(s == 0 ? hp : hp1, opndB(base2, s, nt), o[nt]);
+      for (int nt = 0; nt < NTN; ++nt) o[nt] = mfma<BF16>(s == 0 ? st.h0 : st.h1, opndB(base2, s, nt), o[nt]);
+  };
+  if (NC == 1) {
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const unsigned pk = pack2<BF16>(act_f<ACT>(sa.z[e]), act_f<ACT>(sa.z[e + 1]));
+      if (e < 8) sb.h0[e >> 1] = pk; else sb.h1[(e - 8) >> 1] = pk;
+    }
+    last_gemm2(sb);
+  } else {
+    const std::true_type T{};
+    const std::false_type F{};
+    iter(T, F, 0, sa, sb);
+    int c = 1;
+    for (; c + 2 < NC; c += 2) {
+      iter(T, T, c, sb, sa);
+      iter(T, T, c + 1, sa, sb);
+    }
+    if (c + 2 == NC) {  // one more full iteration, then the last
+      iter(T, T, c, sb, sa);
+      iter(F, T, c + 1, sa, sb);
+      last_gemm2(sb);
+    } else {            // c == NC - 1
+      iter(F, T, c, sb, sa);
+      last_gemm2(sa);
+    }
   }
 
   // ---- epilogue: O tile (C layout: lane = column d, rows 8(i/4) + 4g + i%4) ----
