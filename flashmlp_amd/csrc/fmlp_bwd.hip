@@ -1,19 +1,19 @@
-// FlashMLP unified backward kernel for gfx950 (MI355X).
+// FlashMLP backward kernels for gfx950 (MI355X).
 //
-// One launch, two program roles selected by the workgroup id (flashmlp.py:360-373):
-//   * dW programs (ids [0, n_dw)): per head h, E-tile of 128 columns and a B-range. Four
+// The reference's two program roles (flashmlp.py:360-373), launched as two kernels so each
+// gets its own register allocation (dW: one wave per SIMD, dX: two):
+//   * dW programs (dw_kernel, launched first): per head h, E-tile of 128 columns and a B-range. Four
 //     waves each own 32 of the E-tile's columns. X and dO rows of the B-range are streamed
 //     in 32-row subtiles through an LDS ring and used twice: row-wise as the A operand of
 //     the recomputed Z = X W1c and dH = dO W2c^T (W1c^T, W2c held in registers), and
 //     through ds_read_b64_tr_b16 as the B operand of dW2 += h^T dO and dW1^T += dZ^T X
 //     (flashmlp.py:247-329). h and dZ are cast to the io dtype before those contractions
 //     (flashmlp.py:297-320) and come straight from the MFMA C layout (lane = E column).
-//   * dX programs (ids [n_dw, n_dw + n_dx)): per head and B-tile; recompute Z^T and
+//   * dX programs (dx_kernel): per head and B-tile; recompute Z^T and
 //     dH^T = W2c dO^T per 32-column E-chunk, dZ = dH * act'(Z) cast to the io dtype, and
 //     dX += dZ W1c^T (flashmlp.py:165-244). Same LDS ring and software pipeline as the
 //     forward kernel.
 // Leaky ReLU uses the autograd slope at Z == 0 (0.01); the reference Triton kernel uses 1.
-// dW programs are dispatched first (low ids): they are the long-running ones.
 #include "fmlp_device.h"
 #include "fmlp_launch.h"
 #include <type_traits>
@@ -24,6 +24,8 @@ constexpr int BWD_NW = 4;            // waves per workgroup (both roles)
 constexpr int BWD_NT = BWD_NW * 64;  // threads
 constexpr int DW_ET = 128;           // E columns per dW program (32 per wave)
 constexpr int DW_BT = 32;            // rows per streamed subtile
+// dX workgroups: 4 waves (128 rows).
+__host__ __device__ constexpr int dx_waves(int D) { return D > 0 ? 4 : 4; }
 
 // ------------------------------------------------------------------------------------
 // dW role
@@ -108,22 +110,23 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
     for (int j = 0; j < PPT; ++j) {
       const int p = tid + (j % (PPT / 2)) * BWD_NT;
       const int r = p / (D / 8), q = p % (D / 8);
-      lds_write16(base + (j < PPT / 2 ? 0u : DOOFF) + tile_off<D>(r, q * 8), stg[j]);
+      lds_write16(base + (j < PPT / 2 ? 0u : DOOFF) + w2s_off(r, q), stg[j]);
     }
   };
 
-  // per-lane LDS offsets (slot relative)
-  unsigned offRow[KS];  // row-wise A operand: row l32, columns 16ks + 8g
+  // per-lane LDS offsets (slot relative). Subtiles are stored as D/32 blocks of
+  // [32 rows][32 columns] (w2s_off), so block, row-group and K-step displacements are
+  // immediates and only the lane part needs a register.
+  //   row-wise A operand: row l32, 16-byte piece 2ks + g  -> offRow[ks % 2] + (ks / 2) * 2048
+  unsigned offRow[2];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) offRow[ks] = tile_off<D>(l32, 16 * ks + 8 * g);
-  unsigned offTr[2][2][NTN];  // transposed B operand: rows 16s + 8r + 4g + i16/4, cols 32nt + 16(G%2) + 4(i16%4)
+  for (int kp = 0; kp < 2; ++kp) offRow[kp] = w2s_off(l32, 2 * kp + g);
+  //   transposed B operand: rows 16s + 8r + 4g + i16/4, columns 32nt + 16(G%2) + 4(i16%4)
+  //   -> offTr[r] + nt * 2048 + s * 1024 (the chunk XOR depends on r and g only)
+  unsigned offTr[2];
 #pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int nt = 0; nt < NTN; ++nt)
-        offTr[s2][r][nt] = tile_off<D>(16 * s2 + 8 * r + 4 * g + (i16 >> 2), 32 * nt + 16 * (G & 1) + 4 * (i16 & 3));
+  for (int r = 0; r < 2; ++r)
+    offTr[r] = w2s_off(8 * r + 4 * g + (i16 >> 2), 2 * (G & 1) + ((i16 & 3) >> 1)) + 8u * (i16 & 1);
 
   f32x16 a2[NTN], a1[NTN];  // dW2 (e x d) and dW1^T (e x d) accumulators
 #pragma unroll
@@ -138,8 +141,8 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
     dh = zero16();
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      const u32x4 ax = lds_read16(base + offRow[ks]);
-      const u32x4 ad = lds_read16(base + DOOFF + offRow[ks]);
+      const u32x4 ax = lds_read16(base + offRow[ks & 1] + (ks >> 1) * 2048u);
+      const u32x4 ad = lds_read16(base + DOOFF + offRow[ks & 1] + (ks >> 1) * 2048u);
       z = mfma<BF16>(ax, w1t[ks], z);
       dh = mfma<BF16>(ad, w2r[ks], dh);
     }
@@ -150,9 +153,10 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int nt = 0; nt < NTN; ++nt) {
-        const u32x4 bdo = cat(lds_read_tr(base + DOOFF + offTr[s2][0][nt]), lds_read_tr(base + DOOFF + offTr[s2][1][nt]));
+        const unsigned o0 = offTr[0] + nt * 2048u + s2 * 1024u, o1 = offTr[1] + nt * 2048u + s2 * 1024u;
+        const u32x4 bdo = cat(lds_read_tr(base + DOOFF + o0), lds_read_tr(base + DOOFF + o1));
         a2[nt] = mfma<BF16>(hT[s2], bdo, a2[nt]);
-        const u32x4 bx = cat(lds_read_tr(base + offTr[s2][0][nt]), lds_read_tr(base + offTr[s2][1][nt]));
+        const u32x4 bx = cat(lds_read_tr(base + o0), lds_read_tr(base + o1));
         a1[nt] = mfma<BF16>(dzT[s2], bx, a1[nt]);
       }
   };
@@ -178,13 +182,19 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
     }
     load_sub(nsub > 2 ? 2 : nsub - 1);
     __syncthreads();
-    f32x16 zc, dhc;
-    gemm_zh(0, zc, dhc);
-    u32x4 hp[2], dzp[2];
-    // Iteration k: recompute Z, dH of subtile k+1 (group 1), accumulate dW over subtile
-    // k-1 (group 2) and activate subtile k, as a fixed sequence of steps: one MFMA each,
-    // operand reads PD steps ahead, activation spread over the steps.
-    auto iter = [&](auto G1, auto G2, int k) {
+    // Pipeline state carried between iterations (ping-pong, no copies): Z and dH of the
+    // subtile to activate, and h, dZ of the previous subtile (A operands of the dW products).
+    struct St {
+      f32x16 z, dh;
+      u32x4 h[2], dz[2];
+    };
+    St sa, sb;
+    gemm_zh(0, sa.z, sa.dh);
+    // Iteration k reads `in` (Z, dH of subtile k; h, dZ of subtile k-1) and writes `out`
+    // (Z, dH of subtile k+1; h, dZ of subtile k): recompute Z, dH of subtile k+1 (group 1),
+    // accumulate dW over subtile k-1 (group 2) and activate subtile k, as a fixed sequence of
+    // steps: one MFMA each, operand reads PD steps ahead, activation spread over the steps.
+    auto iter = [&](auto G1, auto G2, int k, St& in, St& out) {
       constexpr bool DO_G1 = decltype(G1)::value;
       constexpr bool DO_G2 = decltype(G2)::value;
       constexpr int N1 = DO_G1 ? 2 * KS : 0, N2 = DO_G2 ? 4 * NTN : 0, NOPS = N1 + N2;
@@ -197,14 +207,12 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
         const int q = sched_index(j, N1, N2);
         if (sched_is_g2(j, N1, N2)) {  // (s, nt, which): which 0 -> dW2 (B = dO^T), 1 -> dW1^T (B = X^T)
           const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1, which = q & 1;
-          const unsigned b = base2 + (which == 0 ? DOOFF : 0u);
-          return cat(lds_read_tr(b + offTr[s2][0][nt]), lds_read_tr(b + offTr[s2][1][nt]));
+          const unsigned bb = base2 + (which == 0 ? DOOFF : 0u) + nt * 2048u + s2 * 1024u;
+          return cat(lds_read_tr(bb + offTr[0]), lds_read_tr(bb + offTr[1]));
         }
         const int ks = q >> 1, which = q & 1;  // which 0 -> Z (A = X), 1 -> dH (A = dO)
-        return lds_read16(base1 + (which ? DOOFF : 0u) + offRow[ks]);
+        return lds_read16(base1 + (which ? DOOFF : 0u) + offRow[ks & 1] + (ks >> 1) * 2048u);
       };
-      f32x16 zn = zero16(), dhn = zero16();
-      u32x4 hc[2], dzc[2];
       float hv[16], dv[16];
       u32x4 ring[PD + 1];
 #pragma unroll
@@ -217,43 +225,48 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
         const int q = sched_index(j, N1, N2);
         if (sched_is_g2(j, N1, N2)) {
           const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1;
-          if ((q & 1) == 0) a2[nt] = mfma<BF16>(hp[s2], cur, a2[nt]);
-          else a1[nt] = mfma<BF16>(dzp[s2], cur, a1[nt]);
+          if ((q & 1) == 0) a2[nt] = mfma<BF16>(in.h[s2], cur, a2[nt]);
+          else a1[nt] = mfma<BF16>(in.dz[s2], cur, a1[nt]);
         } else {
-          const int ks = q >> 1;
-          if ((q & 1) == 0) zn = mfma<BF16>(cur, w1t[ks], zn);
-          else dhn = mfma<BF16>(cur, w2r[ks], dhn);
+          const int ks = q >> 1;  // ks == 0 starts the chain from a literal zero accumulator
+          if ((q & 1) == 0) out.z = mfma<BF16>(cur, w1t[ks], ks == 0 ? zero16() : out.z);
+          else out.dh = mfma<BF16>(cur, w2r[ks], ks == 0 ? zero16() : out.dh);
         }
 #pragma unroll
         for (int e = 0; e < 16; ++e) {
           if (sched_elem_at(e, j, NOPS, 16)) {
-            act_fb<ACT>(zc[e], dhc[e], hv[e], dv[e]);
+            act_fb<ACT>(in.z[e], in.dh[e], hv[e], dv[e]);
             if (e & 1) {
-              hc[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1], hv[e]);
-              dzc[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
+              out.h[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1], hv[e]);
+              out.dz[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
             }
           }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
       __syncthreads();
-      hp[0] = hc[0];
-      hp[1] = hc[1];
-      dzp[0] = dzc[0];
-      dzp[1] = dzc[1];
-      if constexpr (DO_G1) {
-        zc = zn;
-        dhc = dhn;
-      }
     };
     if (nsub == 1) {
-      activate(zc, dhc, hp, dzp);
+      activate(sa.z, sa.dh, sb.h, sb.dz);
+      gemm_dw(0, sb.h, sb.dz);
     } else {
-      iter(std::true_type{}, std::false_type{}, 0);
-      for (int k = 1; k < nsub - 1; ++k) iter(std::true_type{}, std::true_type{}, k);
-      iter(std::false_type{}, std::true_type{}, nsub - 1);
+      const std::true_type T{};
+      const std::false_type F{};
+      iter(T, F, 0, sa, sb);
+      int k = 1;
+      for (; k + 2 < nsub; k += 2) {
+        iter(T, T, k, sb, sa);
+        iter(T, T, k + 1, sa, sb);
+      }
+      if (k + 2 == nsub) {
+        iter(T, T, k, sb, sa);
+        iter(F, T, k + 1, sa, sb);
+        gemm_dw((nsub - 1) & 3, sb.h, sb.dz);
+      } else {
+        iter(F, T, k, sb, sa);
+        gemm_dw((nsub - 1) & 3, sa.h, sa.dz);
+      }
     }
-    gemm_dw((nsub - 1) & 3, hp, dzp);
   }
 
   // ---- epilogue. C layout: lane = column d (32nt + l32), rows e = 8(i/4) + 4g + (i%4) ----
@@ -297,17 +310,17 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
 // ------------------------------------------------------------------------------------
 // dX role
 // ------------------------------------------------------------------------------------
-template <bool BF16, int D, int ACT, int MT>
+template <bool BF16, int D, int ACT, int MT, int DXW>
 __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __restrict__ W1,
                                         const u16* __restrict__ W2, const u16* __restrict__ dO,
                                         u16* __restrict__ dX, int B, int E, int tiles_per_head, int t) {
   constexpr int KS = D / 16, NTN = D / 32;
-  constexpr int BB = BWD_NW * MT * 32;
+  constexpr int BB = DXW * MT * 32;
   constexpr unsigned SLOT = 128u * D;
   constexpr unsigned W2OFF = 64u * D;
   constexpr int NP = 8 * D;
-  constexpr int PPT = NP / BWD_NT;
-  static_assert(NP % (2 * BWD_NT) == 0, "pieces per thread");
+  constexpr int PPT = NP / (DXW * 64);
+  static_assert(NP % (2 * (DXW * 64)) == 0, "pieces per thread");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
@@ -327,12 +340,12 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
     for (int k = 0; k < PPT; ++k) {
       u32x4 v = {0u, 0u, 0u, 0u};
       if (k < PPT / 2) {
-        const int p = tid + k * BWD_NT;
+        const int p = tid + k * (DXW * 64);
         const int d = p >> 2, q = p & 3;
         const int e = c * 32 + q * 8;
         if (e < E) v = *(const u32x4*)(W1h + (size_t)d * E + e);
       } else {
-        const int p = tid + (k - PPT / 2) * BWD_NT;
+        const int p = tid + (k - PPT / 2) * (DXW * 64);
         const int er = p / (D / 8), q = p % (D / 8);
         const int e = c * 32 + er;
         if (e < E) v = *(const u32x4*)(W2h + (size_t)e * D + q * 8);
@@ -345,15 +358,15 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
 #pragma unroll
     for (int k = 0; k < PPT; ++k) {
       if (k < PPT / 2) {
-        const int p = tid + k * BWD_NT;
+        const int p = tid + k * (DXW * 64);
         const int d = p >> 2, q = p & 3;
         u32x2 lo = {stg[k][0], stg[k][1]}, hi = {stg[k][2], stg[k][3]};
         lds_write8(base + w1c_off(d, 2 * q), lo);
         lds_write8(base + w1c_off(d, 2 * q + 1), hi);
       } else {
-        const int p = tid + (k - PPT / 2) * BWD_NT;
+        const int p = tid + (k - PPT / 2) * (DXW * 64);
         const int er = p / (D / 8), q = p % (D / 8);
-        lds_write16(base + W2OFF + tile_off<D>(er, q * 8), stg[k]);
+        lds_write16(base + W2OFF + w2s_off(er, q), stg[k]);
       }
     }
   };
@@ -381,16 +394,17 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
 #pragma unroll
     for (int r = 0; r < 2; ++r)
       offA[kp][r] = w1c_off(16 * kp + 8 * g + 4 * r + (i16 >> 2), 4 * (G & 1) + (i16 & 3));
-  unsigned offW2[KS];  // row-wise read of W2c (A operand of dH^T): row l32, columns 16ks + 8g
+  // row-wise read of W2c (A operand of dH^T): row l32, 16-byte piece 2ks + g = block ks/2, chunk 2(ks%2) + g
+  unsigned offW2[2];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) offW2[ks] = W2OFF + tile_off<D>(l32, 16 * ks + 8 * g);
-  unsigned offW1[2][2][NTN];  // 8-byte reads of W1c (B operand of dX): row 32nt + l32, unit 4s + 2r + g
+  for (int kp = 0; kp < 2; ++kp) offW2[kp] = W2OFF + w2s_off(l32, 2 * kp + g);
+  // 8-byte reads of W1c (B operand of dX): row 32nt + l32, unit 4s + 2r + g; the unit swizzle
+  // of row 32nt + l32 equals that of row l32, so nt only adds 32 rows (2048 bytes)
+  unsigned offW1[2][2];
 #pragma unroll
   for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) offW1[s2][r][nt] = w1c_off(32 * nt + l32, 4 * s2 + 2 * r + g);
+    for (int r = 0; r < 2; ++r) offW1[s2][r] = w1c_off(l32, 4 * s2 + 2 * r + g);
 
   f32x16 acc[MT][NTN];
 #pragma unroll
@@ -409,7 +423,7 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
     for (int ks = 0; ks < KS; ++ks) {
       const u32x4 A = cat(lds_read_tr(base + offA[ks & 1][0] + (ks >> 1) * 2048u),
                           lds_read_tr(base + offA[ks & 1][1] + (ks >> 1) * 2048u));
-      const u32x4 A2 = lds_read16(base + offW2[ks]);
+      const u32x4 A2 = lds_read16(base + offW2[ks & 1] + (ks >> 1) * 2048u);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         z[mt] = mfma<BF16>(A, xr[mt][ks], z[mt]);
@@ -423,7 +437,7 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
       for (int nt = 0; nt < NTN; ++nt) {
-        const u32x4 Bv = cat(lds_read8(base + offW1[s2][0][nt]), lds_read8(base + offW1[s2][1][nt]));
+        const u32x4 Bv = cat(lds_read8(base + offW1[s2][0] + nt * 2048u), lds_read8(base + offW1[s2][1] + nt * 2048u));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma<BF16>(dzA[mt][s2], Bv, acc[mt][nt]);
       }
@@ -447,17 +461,23 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
   }
   load_chunk(NC > 2 ? 2 : NC - 1);
   __syncthreads();
-  f32x16 zc[MT], dhc[MT];
-  gemm_zh(0, zc, dhc);
-  u32x4 dzp[MT][2];
-  // Iteration c: recompute Z^T, dH^T of chunk c+1 (group 1), accumulate dX over chunk c-1
-  // (group 2) and form dZ of chunk c, as a fixed sequence of steps (see the dW role).
-  auto iter = [&](auto G1, auto G2, int c) {
+  // Pipeline state carried between iterations (ping-pong, no copies): Z^T and dH^T of the
+  // chunk to activate and dZ of the previous chunk (A operand of dX += dZ W1c^T).
+  struct St {
+    f32x16 z[MT], dh[MT];
+    u32x4 dz[MT][2];
+  };
+  St sa, sb;
+  gemm_zh(0, sa.z, sa.dh);
+  // Iteration c reads `in` (Z^T, dH^T of chunk c; dZ of chunk c-1) and writes `out`:
+  // recompute Z^T, dH^T of chunk c+1 (group 1), accumulate dX over chunk c-1 (group 2) and
+  // form dZ of chunk c, as a fixed sequence of steps (see the dW role).
+  auto iter = [&](auto G1, auto G2, int c, St& in, St& out) {
     constexpr bool DO_G1 = decltype(G1)::value;
     constexpr bool DO_G2 = decltype(G2)::value;
     constexpr int N1 = DO_G1 ? 2 * KS : 0, N2 = DO_G2 ? 2 * NTN : 0, NOPS = N1 + N2;
     constexpr int NEL = 16 * MT;
-    constexpr int PD = 3;
+    constexpr int PD = 2;
     const unsigned base1 = ((c + 1) & 3) * SLOT, base2 = ((c - 1) & 3) * SLOT;
     store_chunk((c + 2) & 3);                  // chunk c+2 (loaded during iteration c-1)
     load_chunk(c + 3 < NC ? c + 3 : NC - 1);   // chunk c+3 -> registers
@@ -466,21 +486,14 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
       const int q = sched_index(j, N1, N2);
       if (sched_is_g2(j, N1, N2)) {  // dX += dZ W1c^T: B = W1c rows (e-runs of 4)
         const int s2 = q / NTN, nt = q % NTN;
-        return cat(lds_read8(base2 + offW1[s2][0][nt]), lds_read8(base2 + offW1[s2][1][nt]));
+        return cat(lds_read8(base2 + offW1[s2][0] + nt * 2048u), lds_read8(base2 + offW1[s2][1] + nt * 2048u));
       }
       const int ks = q >> 1;
       if ((q & 1) == 0)  // Z^T: A = W1c^T (transposed read)
         return cat(lds_read_tr(base1 + offA[ks & 1][0] + (ks >> 1) * 2048u),
                    lds_read_tr(base1 + offA[ks & 1][1] + (ks >> 1) * 2048u));
-      return lds_read16(base1 + offW2[ks]);  // dH^T: A = W2c rows
+      return lds_read16(base1 + offW2[ks & 1] + (ks >> 1) * 2048u);  // dH^T: A = W2c rows
     };
-    f32x16 zn[MT], dhn[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      zn[mt] = zero16();
-      dhn[mt] = zero16();
-    }
-    u32x4 dzc[MT][2];
     float dv[NEL];
     u32x4 ring[PD + 1];
 #pragma unroll
@@ -494,44 +507,49 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
       if (sched_is_g2(j, N1, N2)) {
         const int s2 = q / NTN, nt = q % NTN;
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma<BF16>(dzp[mt][s2], cur, acc[mt][nt]);
+        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma<BF16>(in.dz[mt][s2], cur, acc[mt][nt]);
       } else {
         const int ks = q >> 1;
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          if ((q & 1) == 0) zn[mt] = mfma<BF16>(cur, xr[mt][ks], zn[mt]);
-          else dhn[mt] = mfma<BF16>(cur, dr[mt][ks], dhn[mt]);
+          // ks == 0 starts the chain from a literal zero accumulator
+          if ((q & 1) == 0) out.z[mt] = mfma<BF16>(cur, xr[mt][ks], ks == 0 ? zero16() : out.z[mt]);
+          else out.dh[mt] = mfma<BF16>(cur, dr[mt][ks], ks == 0 ? zero16() : out.dh[mt]);
         }
       }
 #pragma unroll
       for (int e = 0; e < NEL; ++e) {
         if (sched_elem_at(e, j, NOPS, NEL)) {
           const int mt = e >> 4, i = e & 15;
-          dv[e] = act_b<ACT>(zc[mt][i], dhc[mt][i]);
-          if (e & 1) dzc[mt][i >> 3][(i >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
+          dv[e] = act_b<ACT>(in.z[mt][i], in.dh[mt][i]);
+          if (e & 1) out.dz[mt][i >> 3][(i >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
     }
     __syncthreads();
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      dzp[mt][0] = dzc[mt][0];
-      dzp[mt][1] = dzc[mt][1];
-      if constexpr (DO_G1) {
-        zc[mt] = zn[mt];
-        dhc[mt] = dhn[mt];
-      }
-    }
   };
   if (NC == 1) {
-    activate(zc, dhc, dzp);
+    activate(sa.z, sa.dh, sb.dz);
+    gemm_dx(0, sb.dz);
   } else {
-    iter(std::true_type{}, std::false_type{}, 0);
-    for (int c = 1; c < NC - 1; ++c) iter(std::true_type{}, std::true_type{}, c);
-    iter(std::false_type{}, std::true_type{}, NC - 1);
+    const std::true_type T{};
+    const std::false_type F{};
+    iter(T, F, 0, sa, sb);
+    int c = 1;
+    for (; c + 2 < NC; c += 2) {
+      iter(T, T, c, sb, sa);
+      iter(T, T, c + 1, sa, sb);
+    }
+    if (c + 2 == NC) {
+      iter(T, T, c, sb, sa);
+      iter(F, T, c + 1, sa, sb);
+      gemm_dx((NC - 1) & 3, sb.dz);
+    } else {
+      iter(F, T, c, sb, sa);
+      gemm_dx((NC - 1) & 3, sa.dz);
+    }
   }
-  gemm_dx((NC - 1) & 3, dzp);
 
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -545,19 +563,25 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
     }
 }
 
-template <bool BF16, int D, int ACT, int MT>
+// dW programs: one wave per SIMD (the role keeps W1c^T / W2c fragments and both dW
+// accumulators in registers).
+template <bool BF16, int D, int ACT>
 __global__ void __launch_bounds__(BWD_NT)
-bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-           const u16* __restrict__ dO, u16* __restrict__ dX, u16* __restrict__ dW1, u16* __restrict__ dW2,
-           float* __restrict__ ws, int H, int B, int E, int nE, int nS, int rows_per_split, int n_dw,
-           int dx_tiles_per_head) {
-  const int bid = blockIdx.x;
-  if (bid < n_dw) {
-    dw_role<BF16, D, ACT>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, xcd_remap(bid, n_dw));
-  } else {
-    const int n_dx = (int)gridDim.x - n_dw;
-    dx_role<BF16, D, ACT, MT>(X, W1, W2, dO, dX, B, E, dx_tiles_per_head, xcd_remap(bid - n_dw, n_dx));
-  }
+dw_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+          const u16* __restrict__ dO, u16* __restrict__ dW1, u16* __restrict__ dW2, float* __restrict__ ws,
+          int H, int B, int E, int nE, int nS, int rows_per_split) {
+  dw_role<BF16, D, ACT>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split,
+                        xcd_remap(blockIdx.x, gridDim.x));
+}
+
+// dX programs: 4 waves; at D = 64 two workgroups share a CU (two waves per SIMD), at
+// D = 128 the role needs more than 256 VGPRs and runs one wave per SIMD.
+template <bool BF16, int D, int ACT, int MT>
+__global__ void __launch_bounds__(dx_waves(D) * 64)
+dx_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+          const u16* __restrict__ dO, u16* __restrict__ dX, int B, int E, int tiles_per_head) {
+  dx_role<BF16, D, ACT, MT, dx_waves(D)>(X, W1, W2, dO, dX, B, E, tiles_per_head,
+                                         xcd_remap(blockIdx.x, gridDim.x));
 }
 
 // Sum of the nS fp32 partials; dW2 keeps the (e, d) layout, dW1 is written transposed.
@@ -605,8 +629,9 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus) {
   // dX programs: 256 rows when that still gives >= 2 programs per CU, else 128
   // (D = 128 with two M-tiles per wave exceeds the register file, so it keeps one)
   const long long big = (B + 255) / 256 * H;
-  p.dx_mt = (D == 64 && big >= 2LL * num_cus) ? 2 : 1;
-  const int rows = BWD_NW * 32 * p.dx_mt;
+  (void)big;
+  p.dx_mt = 1;
+  const int rows = dx_waves((int)D) * 32 * p.dx_mt;
   p.dx_tiles_per_head = (int)((B + rows - 1) / rows);
   p.n_dw = base * p.nS;
   p.n_dx = (long long)p.dx_tiles_per_head * H;
@@ -616,38 +641,43 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus) {
 
 template <bool BF16, int D, int ACT>
 static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
-  const long long grid = p.n_dw + p.n_dx;
-  if (grid <= 0) return hipSuccess;
-  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  const size_t lds_dw = 4u * 128u * D > (size_t)D * DW_ET * 2 ? 4u * 128u * D : (size_t)D * DW_ET * 2;
-  const size_t lds = lds_dw;  // the dX ring (4 * 128 * D) is the same size
+  if (p.n_dw > 0x7fffffffLL || p.n_dx > 0x7fffffffLL) return hipErrorInvalidValue;
   hipError_t e;
-  if (D == 64 && p.dx_mt == 2) {
-    auto k = bwd_kernel<BF16, D, ACT, (D == 64 ? 2 : 1)>;
+  // dW programs (and their partial reduction), then dX programs, in stream order
+  if (p.n_dw > 0) {
+    const size_t lds = 4u * 128u * D > (size_t)D * DW_ET * 2 ? 4u * 128u * D : (size_t)D * DW_ET * 2;
+    auto k = dw_kernel<BF16, D, ACT>;
     e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(BWD_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                       (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dx, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws,
-                       (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw, p.dx_tiles_per_head);
-  } else {
-    auto k = bwd_kernel<BF16, D, ACT, 1>;
-    e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(BWD_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                       (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dx, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws,
-                       (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw, p.dx_tiles_per_head);
-  }
-  e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  if (p.nS > 1) {
-    const size_t per = (size_t)a.H * a.E * a.D;
-    size_t blocks = (per + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws,
-                       (u16*)a.dw1, (u16*)a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS);
+    hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(BWD_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                       (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws, (int)a.H,
+                       (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split);
     e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (p.nS > 1) {
+      const size_t per = (size_t)a.H * a.E * a.D;
+      size_t blocks = (per + 255) / 256;
+      if (blocks > 8192) blocks = 8192;
+      hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws,
+                         (u16*)a.dw1, (u16*)a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
   }
-  return e;
+  if (p.n_dx > 0) {
+    const size_t lds = 4u * 128u * D;
+    auto launch = [&](auto k) {
+      hipError_t r = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (r != hipSuccess) return r;
+      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(dx_waves(D) * 64), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                         (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head);
+      return hipGetLastError();
+    };
+    if (D == 64 && p.dx_mt == 2) e = launch(dx_kernel<BF16, D, ACT, (D == 64 ? 2 : 1)>);
+    else e = launch(dx_kernel<BF16, D, ACT, 1>);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 template <bool BF16, int D>

@@ -141,23 +141,27 @@ __device__ __forceinline__ float act_b(float z, float dh) {
 }
 
 // ---------------------------------------------------------------------------------
-// LDS access helpers (byte offsets into dynamic shared memory, which starts at 0).
+// LDS access helpers. Kernels use dynamic shared memory only, addressed by byte offset
+// from its start. Offsets are signed and applied as in-bounds pointer arithmetic, which
+// lets the compiler move constant parts into the DS instructions' immediate offset field.
 // ---------------------------------------------------------------------------------
-__device__ __forceinline__ u32x4 lds_read16(unsigned byte_off) {
-  return *(const FMLP_LDS u32x4*)(byte_off);
+extern __shared__ __attribute__((aligned(16))) char fmlp_lds[];
+
+__device__ __forceinline__ u32x4 lds_read16(int byte_off) {
+  return *(const FMLP_LDS u32x4*)((FMLP_LDS char*)fmlp_lds + byte_off);
 }
-__device__ __forceinline__ u32x2 lds_read8(unsigned byte_off) {
-  return *(const FMLP_LDS u32x2*)(byte_off);
+__device__ __forceinline__ u32x2 lds_read8(int byte_off) {
+  return *(const FMLP_LDS u32x2*)((FMLP_LDS char*)fmlp_lds + byte_off);
 }
-__device__ __forceinline__ u32x2 lds_read_tr(unsigned byte_off) {
-  i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLP_LDS i16x4*)(byte_off));
+__device__ __forceinline__ u32x2 lds_read_tr(int byte_off) {
+  i16x4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FMLP_LDS i16x4*)((FMLP_LDS char*)fmlp_lds + byte_off));
   return __builtin_bit_cast(u32x2, r);
 }
-__device__ __forceinline__ void lds_write16(unsigned byte_off, const u32x4& v) {
-  *(FMLP_LDS u32x4*)(byte_off) = v;
+__device__ __forceinline__ void lds_write16(int byte_off, const u32x4& v) {
+  *(FMLP_LDS u32x4*)((FMLP_LDS char*)fmlp_lds + byte_off) = v;
 }
-__device__ __forceinline__ void lds_write8(unsigned byte_off, const u32x2& v) {
-  *(FMLP_LDS u32x2*)(byte_off) = v;
+__device__ __forceinline__ void lds_write8(int byte_off, const u32x2& v) {
+  *(FMLP_LDS u32x2*)((FMLP_LDS char*)fmlp_lds + byte_off) = v;
 }
 __device__ __forceinline__ u32x4 cat(const u32x2& lo, const u32x2& hi) {
   u32x4 r = {lo[0], lo[1], hi[0], hi[1]};
@@ -186,6 +190,13 @@ __device__ __forceinline__ unsigned tile_off(unsigned r, unsigned d) {
 // is stored at unit u ^ ((r >> 2) & 7): conflict free for both patterns.
 __device__ __forceinline__ unsigned w1c_off(unsigned r, unsigned unit) {
   return r * 64u + ((unit ^ ((r >> 2) & 7u)) << 3);
+}
+
+// W2 chunk tile [32 rows][D] stored as D/32 blocks of [32 rows][32 columns] (64-byte rows),
+// read row-wise (lane m reads row m, one 16-byte piece). 16-byte piece q of row r (q < D/8)
+// lives in block q/4 at chunk (q%4) ^ ((r >> 2) & 3): conflict free for 16 consecutive rows.
+__device__ __forceinline__ unsigned w2s_off(unsigned r, unsigned q) {
+  return (q >> 2) * 2048u + r * 64u + (((q & 3u) ^ ((r >> 2) & 3u)) << 4);
 }
 
 // ---------------------------------------------------------------------------------

@@ -153,7 +153,6 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       const int k = idx(j);
       return is_g1(j) ? opndA(base1, k) : opndB(base2, k / NTN, k % NTN);
     };
-    if constexpr (DO_G1) out.z = zero16();
     u32x4 op0 = fetch(0), op1 = NOPS > 1 ? fetch(1) : op0, op2 = op0;
     float hv[16];
     __builtin_amdgcn_sched_barrier(0);
@@ -165,8 +164,8 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
         if ((j + 2) % 3 == 0) op0 = nx; else if ((j + 2) % 3 == 1) op1 = nx; else op2 = nx;
       }
       const int k = idx(j);
-      if (is_g1(j)) {
-        out.z = mfma<BF16>(cur, xr[k], out.z);
+      if (is_g1(j)) {  // k == 0 starts the chain from a literal zero accumulator
+        out.z = mfma<BF16>(cur, xr[k], k == 0 ? zero16() : out.z);
       } else {
         const int s = k / NTN, nt = k % NTN;
         o[nt] = mfma<BF16>(s == 0 ? in.h0 : in.h1, cur, o[nt]);
