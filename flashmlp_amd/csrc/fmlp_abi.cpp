@@ -73,6 +73,9 @@ int check_shape(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   if (B > (1LL << 30) || E > (1LL << 30) || H > (1LL << 30))
     return fail(FMLP_ERR_INVALID_ARG, "dimension too large (H=%lld B=%lld E=%lld)", (long long)H, (long long)B,
                 (long long)E);
+  // the kernels address one head's W1 / W2 (D x E values) with 32-bit byte offsets
+  if (D * E * 2 > 0x7fffffffLL)
+    return fail(FMLP_ERR_UNSUPPORTED, "per-head weight slice D*E=%lld values exceeds 2 GiB", (long long)(D * E));
   // every tile count must fit a 32-bit grid
   if (H * ((B + 127) / 128) + H * ((E + 127) / 128) * 64 > 0x7fffffffLL)
     return fail(FMLP_ERR_INVALID_ARG, "problem too large for one launch");

@@ -91,17 +91,24 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
   __syncthreads();  // the W1 staging area becomes the subtile ring
 
   // ---- subtile staging ----
+  // Branch-free buffer loads over the subtile's rows: rows past the B-range (and whole
+  // subtiles past the last one, loaded but never used) fall outside the resource.
   u32x4 stg[PPT];
-  auto load_sub = [&](int k) {
+  unsigned offSub[PPT / 2];
 #pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-      const int p = tid + (j % (PPT / 2)) * BWD_NT;
-      const int r = p / (D / 8), q = p % (D / 8);
-      const int b = b_lo + k * DW_BT + r;
-      const u16* src = (j < PPT / 2) ? Xh : dOh;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (b < b_hi) v = *(const u32x4*)(src + (size_t)b * D + q * 8);
-      stg[j] = v;
+  for (int j = 0; j < PPT / 2; ++j) {
+    const unsigned p = tid + j * BWD_NT;
+    offSub[j] = (p / (D / 8)) * (D * 2u) + (p % (D / 8)) * 16u;  // row r, piece q
+  }
+  auto load_sub = [&](int k) {
+    const int r0 = b_lo + k * DW_BT;
+    const long long bytes = (long long)min(max(b_hi - r0, 0), DW_BT) * D * 2;
+    const Rsrc rx = make_rsrc(Xh + (size_t)r0 * D, bytes);
+    const Rsrc rd = make_rsrc(dOh + (size_t)r0 * D, bytes);
+#pragma unroll
+    for (int j = 0; j < PPT / 2; ++j) {
+      stg[j] = buf_load16(rx, offSub[j]);
+      stg[PPT / 2 + j] = buf_load16(rd, offSub[j]);
     }
   };
   auto store_sub = [&](int slot) {
@@ -180,7 +187,7 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
       load_sub(1);
       store_sub(1);
     }
-    load_sub(nsub > 2 ? 2 : nsub - 1);
+    load_sub(2);
     __syncthreads();
     // Pipeline state carried between iterations (ping-pong, no copies): Z and dH of the
     // subtile to activate, and h, dZ of the previous subtile (A operands of the dW products).
@@ -198,10 +205,10 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
       constexpr bool DO_G1 = decltype(G1)::value;
       constexpr bool DO_G2 = decltype(G2)::value;
       constexpr int N1 = DO_G1 ? 2 * KS : 0, N2 = DO_G2 ? 4 * NTN : 0, NOPS = N1 + N2;
-      constexpr int PD = 3;
+      constexpr int PD = 2;
       const unsigned base1 = ((k + 1) & 3) * SLOT, base2 = ((k - 1) & 3) * SLOT;
       store_sub((k + 2) & 3);                    // subtile k+2 (loaded during iteration k-1)
-      load_sub(k + 3 < nsub ? k + 3 : nsub - 1);  // subtile k+3 -> registers
+      load_sub(k + 3);  // subtile k+3 -> registers
       __builtin_amdgcn_sched_barrier(0);
       auto fetch = [&](int j) -> u32x4 {
         const int q = sched_index(j, N1, N2);
@@ -233,13 +240,11 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
           else out.dh = mfma<BF16>(cur, w2r[ks], ks == 0 ? zero16() : out.dh);
         }
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          if (sched_elem_at(e, j, NOPS, 16)) {
-            act_fb<ACT>(in.z[e], in.dh[e], hv[e], dv[e]);
-            if (e & 1) {
-              out.h[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1], hv[e]);
-              out.dz[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
-            }
+        for (int e = sched_elem_begin(j, NOPS, 16); e < sched_elem_begin(j + 1, NOPS, 16); ++e) {
+          act_fb<ACT>(in.z[e], in.dh[e], hv[e], dv[e]);
+          if (e & 1) {
+            out.h[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1], hv[e]);
+            out.dz[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
           }
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -334,23 +339,26 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
   u16* dXh = dX + (size_t)h * B * D;
   const int b_wave = bt * BB + wave * MT * 32;
 
+  // Branch-free buffer loads (as in the forward kernel): W2c rows past E fall outside the
+  // chunk's resource, W1c columns past E get an out-of-range offset, chunks past the last
+  // one are loaded but never used.
   u32x4 stg[PPT];
-  auto load_chunk = [&](int c) {
+  const unsigned colq = (tid & 3) * 8;
+  unsigned offW1g[PPT / 2], offW2g[PPT / 2];
 #pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (k < PPT / 2) {
-        const int p = tid + k * (DXW * 64);
-        const int d = p >> 2, q = p & 3;
-        const int e = c * 32 + q * 8;
-        if (e < E) v = *(const u32x4*)(W1h + (size_t)d * E + e);
-      } else {
-        const int p = tid + (k - PPT / 2) * (DXW * 64);
-        const int er = p / (D / 8), q = p % (D / 8);
-        const int e = c * 32 + er;
-        if (e < E) v = *(const u32x4*)(W2h + (size_t)e * D + q * 8);
-      }
-      stg[k] = v;
+  for (int k = 0; k < PPT / 2; ++k) {
+    const unsigned p = tid + k * (DXW * 64);
+    offW1g[k] = (p >> 2) * (unsigned)E * 2u + (p & 3u) * 16u;           // row d, piece q
+    offW2g[k] = (p / (D / 8)) * (D * 2u) + (p % (D / 8)) * 16u;          // row er, piece q
+  }
+  auto load_chunk = [&](int c) {
+    const int lim = E - c * 32;
+    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, (long long)D * E * 2 - 64LL * c);
+    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, (long long)min(max(lim, 0), 32) * D * 2);
+#pragma unroll
+    for (int k = 0; k < PPT / 2; ++k) {
+      stg[k] = buf_load16(r1, (int)colq < lim ? offW1g[k] : BUF_OOB);
+      stg[PPT / 2 + k] = buf_load16(r2, offW2g[k]);
     }
   };
   auto store_chunk = [&](int slot) {
@@ -459,7 +467,7 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
     load_chunk(1);
     store_chunk(1);
   }
-  load_chunk(NC > 2 ? 2 : NC - 1);
+  load_chunk(2);
   __syncthreads();
   // Pipeline state carried between iterations (ping-pong, no copies): Z^T and dH^T of the
   // chunk to activate and dZ of the previous chunk (A operand of dX += dZ W1c^T).
@@ -480,7 +488,7 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
     constexpr int PD = 2;
     const unsigned base1 = ((c + 1) & 3) * SLOT, base2 = ((c - 1) & 3) * SLOT;
     store_chunk((c + 2) & 3);                  // chunk c+2 (loaded during iteration c-1)
-    load_chunk(c + 3 < NC ? c + 3 : NC - 1);   // chunk c+3 -> registers
+    load_chunk(c + 3);  // chunk c+3 -> registers
     __builtin_amdgcn_sched_barrier(0);
     auto fetch = [&](int j) -> u32x4 {
       const int q = sched_index(j, N1, N2);
@@ -518,12 +526,10 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
         }
       }
 #pragma unroll
-      for (int e = 0; e < NEL; ++e) {
-        if (sched_elem_at(e, j, NOPS, NEL)) {
-          const int mt = e >> 4, i = e & 15;
-          dv[e] = act_b<ACT>(in.z[mt][i], in.dh[mt][i]);
-          if (e & 1) out.dz[mt][i >> 3][(i >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
-        }
+      for (int e = sched_elem_begin(j, NOPS, NEL); e < sched_elem_begin(j + 1, NOPS, NEL); ++e) {
+        const int mt = e >> 4, i = e & 15;
+        dv[e] = act_b<ACT>(in.z[mt][i], in.dh[mt][i]);
+        if (e & 1) out.dz[mt][i >> 3][(i >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }

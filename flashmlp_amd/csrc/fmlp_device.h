@@ -168,6 +168,25 @@ __device__ __forceinline__ u32x4 cat(const u32x2& lo, const u32x2& hi) {
   return r;
 }
 
+// ---------------------------------------------------------------------------------
+// Raw buffer loads (stride-0 buffer resource). A load at a byte offset at or beyond the
+// resource's size returns zeros without touching memory, so the edge tiles of a loop need
+// no branches: the loop body stays one basic block and the compiler keeps the
+// instruction order the step schedules ask for. Word 3 0x00020000 is the gfx9-family
+// resource format (32-bit data format, no swizzle, no index stride).
+// ---------------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t Rsrc;
+constexpr unsigned BUF_OOB = 0x80000000u;  // an offset beyond every resource make_rsrc builds
+
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, long long bytes) {
+  // the size is wave-uniform; readfirstlane keeps the resource in scalar registers
+  const int n = __builtin_amdgcn_readfirstlane(bytes <= 0 ? 0 : (bytes >= 0x7fffffffLL ? 0x7fffffff : (int)bytes));
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(Rsrc r, unsigned byte_off) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
+}
+
 // Row swizzle for row-major tiles whose rows are D 16-bit values (D = 64 or 128) and that
 // are read both row-wise (16-byte chunks, lane m reads row m) and with ds_read_b64_tr_b16
 // over 4-row x 32-byte blocks. 16-byte chunk c of row r is stored at chunk c ^ swz(r).
@@ -211,9 +230,13 @@ __device__ __forceinline__ constexpr bool sched_is_g2(int j, int n1, int n2) {
 __device__ __forceinline__ constexpr int sched_index(int j, int n1, int n2) {
   return sched_is_g2(j, n1, n2) ? sched_g2_before(j, n1, n2) : j - sched_g2_before(j, n1, n2);
 }
-// element e of an iteration's n_elem activations is computed at step (e * nsteps) / n_elem
-__device__ __forceinline__ constexpr bool sched_elem_at(int e, int j, int nsteps, int n_elem) {
-  return (e * nsteps) / n_elem == j;
+// Element e of an iteration's n_elem activations is computed at step (e * nsteps) / n_elem,
+// i.e. step j computes elements [sched_elem_begin(j), sched_elem_begin(j + 1)). Loops over
+// a step's elements take these bounds so that the element index depends on the step: an
+// activation that did not would be loop invariant in the (not yet unrolled) step loop and
+// could be hoisted out of it, which collapses the interleave.
+__device__ __forceinline__ constexpr int sched_elem_begin(int j, int nsteps, int n_elem) {
+  return (j * n_elem + nsteps - 1) / nsteps;
 }
 
 // ---------------------------------------------------------------------------------

@@ -52,22 +52,26 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const int b_wave = bt * BB + wave * 32;
 
   // ---- chunk staging: global -> registers (one chunk ahead) -> LDS ----
+  // Branch-free buffer loads: W2c rows past E fall outside the chunk's resource; W1c
+  // columns past E (last chunk when E % 32 != 0) get an out-of-range offset. Chunks past
+  // the last one are loaded but never used.
   u32x4 stg[PPT];
-  auto load_chunk = [&](int c) {
+  const unsigned colq = (tid & 3) * 8;  // first column of this thread's W1c pieces
+  unsigned offW1g[PPT / 2], offW2g[PPT / 2];
 #pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      u32x4 v = {0u, 0u, 0u, 0u};
-      const int p = tid + (k % (PPT / 2)) * NT;
-      if (k < PPT / 2) {  // W1c: row d, 16-byte piece q
-        const int d = p >> 2, q = p & 3;
-        const int e = c * 32 + q * 8;
-        if (e < E) v = *(const u32x4*)(W1h + (size_t)d * E + e);
-      } else {            // W2c: block nt, row er, 16-byte piece q
-        const int q = p & 3, er = (p >> 2) & 31, nt = p >> 7;
-        const int e = c * 32 + er;
-        if (e < E) v = *(const u32x4*)(W2h + (size_t)e * D + nt * 32 + q * 8);
-      }
-      stg[k] = v;
+  for (int k = 0; k < PPT / 2; ++k) {
+    const unsigned p = tid + k * NT;
+    offW1g[k] = (p >> 2) * (unsigned)E * 2u + (p & 3u) * 16u;                   // row d, piece q
+    offW2g[k] = ((p >> 2) & 31u) * (D * 2u) + (p >> 7) * 64u + (p & 3u) * 16u;   // row er, block nt, piece q
+  }
+  auto load_chunk = [&](int c) {
+    const int lim = E - c * 32;
+    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, (long long)D * E * 2 - 64LL * c);
+    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, (long long)min(max(lim, 0), 32) * D * 2);
+#pragma unroll
+    for (int k = 0; k < PPT / 2; ++k) {
+      stg[k] = buf_load16(r1, (int)colq < lim ? offW1g[k] : BUF_OOB);
+      stg[PPT / 2 + k] = buf_load16(r2, offW2g[k]);
     }
   };
   auto store_chunk = [&](int slot) {
@@ -117,7 +121,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     load_chunk(1);
     store_chunk(1);
   }
-  load_chunk(NC > 2 ? 2 : NC - 1);
+  load_chunk(2);
   __syncthreads();
   // Pipeline state carried between iterations: Z^T of the chunk to activate and h of the
   // previous chunk (A operand of O += h W2c, two K steps). Iterations run in pairs with the
@@ -142,8 +146,8 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     constexpr int PER = 16 / NOPS;  // activation elements per step
     const unsigned base1 = ((c + 1) & 3) * SLOT, base2 = ((c - 1) & 3) * SLOT;
 
-    store_chunk((c + 2) & 3);                  // chunk c+2 (loaded during iteration c-1)
-    load_chunk(c + 3 < NC ? c + 3 : NC - 1);   // chunk c+3 -> registers
+    store_chunk((c + 2) & 3);  // chunk c+2 (loaded during iteration c-1)
+    load_chunk(c + 3);         // chunk c+3 -> registers
     __builtin_amdgcn_sched_barrier(0);
 
     // op j: G1 and G2 alternate when both are present
