@@ -569,6 +569,236 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
     }
 }
 
+// ------------------------------------------------------------------------------------
+// dX programs, two-waves-per-SIMD form (dx2_kernel): 8 waves x 32 rows = 256 rows of one
+// head. Per 32-column E-chunk c each wave runs two phases:
+//   MFMA phase: Z^T(c) = W1c^T X^T and dH^T(c) = W2c dO^T (16 MFMAs) interleaved with
+//               dX += dZ(c-1) W1c(c-1)^T (8 MFMAs), operand reads three steps ahead;
+//   VALU phase: dZ(c) = dH * act'(Z) for the wave's 32 x 32 tile, cast to the io dtype.
+// Waves 0-3 run MFMA-then-VALU, waves 4-7 VALU(c-1)-then-MFMA, so the two waves sharing a
+// SIMD keep the matrix cores and the VALU busy at the same time (the per-chunk barrier
+// would otherwise align them). Nothing is double-buffered in registers, which keeps a wave
+// within 256 VGPRs. W1c / W2c chunks go from memory straight into a 4-slot LDS ring
+// (buffer loads to LDS, two chunks ahead).
+//
+// E-order inside a chunk: Z^T row m holds chunk column e = sig(m) (bits 2 and 3 of m
+// swapped). Then the 8 k-slots a lane holds of the dZ operand (C layout rows
+// 16 s + 8 (j / 4) + 4 g + j % 4) are 8 consecutive columns 16 s + 8 g + j, and the W1c
+// operand of dX is one 16-byte row read. The transposed W1c^T read and the W2c row read
+// pick their columns / rows in the same order.
+//
+// LDS slot (128 D bytes): W1c [D rows d][32 columns e] 64-byte rows, 16-byte chunk q of row
+// r at chunk q ^ ((r >> 2) & 3); then W2c [32 rows e][D] as D/32 blocks of [32][32]
+// (w2s_off). Both are written by lane-linear 16-byte DMA pieces; each lane loads the
+// global piece that belongs at its LDS position.
+// ------------------------------------------------------------------------------------
+__device__ __forceinline__ constexpr unsigned sig(unsigned m) {
+  return (m & ~12u) | ((m & 4u) << 1) | ((m & 8u) >> 1);
+}
+
+constexpr int DX2_NW = 8;
+constexpr int DX2_NT = DX2_NW * 64;
+constexpr int DX2_ROWS = DX2_NW * 32;
+
+template <bool BF16, int D, int ACT>
+__global__ void __launch_bounds__(DX2_NT)
+dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+           const u16* __restrict__ dO, u16* __restrict__ dX, int B, int E, int tiles_per_head) {
+  constexpr int KS = D / 16, NTN = D / 32;
+  constexpr unsigned SLOT = 128u * D;
+  constexpr unsigned W2OFF = 64u * D;
+  constexpr int NDMA = D / 64;  // 1 KB DMA instructions per wave per chunk
+  constexpr int N1 = 2 * KS, N2 = 2 * NTN;
+  constexpr int PD = 3;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
+  const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
+  const int NC = (E + 31) >> 5;
+  const bool late = wave >= 4;  // VALU-first half of the workgroup
+
+  const u16* Xh = X + (size_t)h * B * D;
+  const u16* dOh = dO + (size_t)h * B * D;
+  const u16* W1h = W1 + (size_t)h * D * E;
+  const u16* W2h = W2 + (size_t)h * E * D;
+  u16* dXh = dX + (size_t)h * B * D;
+  const int b_wave = bt * DX2_ROWS + wave * 32;
+
+  // ---- DMA pieces: piece p (16 bytes at slot offset 16 p) of a chunk ----
+  unsigned dmaOff[NDMA];
+  int dmaCol[NDMA];  // W1c pieces: first chunk column (masked against E); W2c pieces: -1
+#pragma unroll
+  for (int k = 0; k < NDMA; ++k) {
+    const unsigned p = k * DX2_NT + wave * 64 + lane;
+    if (p < 4u * D) {  // W1c row r, logical chunk q
+      const unsigned r = p >> 2, q = (p & 3u) ^ ((r >> 2) & 3u);
+      dmaOff[k] = r * (unsigned)E * 2u + q * 16u;
+      dmaCol[k] = (int)(q * 8u);
+    } else {           // W2c block bk, row rr, logical piece q
+      const unsigned pp = p - 4u * D, bk = pp >> 7, rr = (pp >> 2) & 31u;
+      const unsigned q = bk * 4u + ((pp & 3u) ^ ((rr >> 2) & 3u));
+      dmaOff[k] = rr * (D * 2u) + q * 16u;
+      dmaCol[k] = -1;
+    }
+  }
+  auto issue_chunk = [&](int c) {
+    const int lim = E - c * 32;
+    const i32x4 r1 = make_rsrc_words(W1h + (size_t)c * 32, (long long)D * E * 2 - 64LL * c);
+    const i32x4 r2 = make_rsrc_words(W2h + (size_t)c * 32 * D, (long long)min(max(lim, 0), 32) * D * 2);
+    const int dst = (c & 3) * (int)SLOT + wave * 1024;
+#pragma unroll
+    for (int k = 0; k < NDMA; ++k) {
+      const bool w1 = (unsigned)(k * DX2_NT + wave * 64) < 4u * D;  // wave-uniform
+      const unsigned off = w1 ? (dmaCol[k] < lim ? dmaOff[k] : BUF_OOB) : dmaOff[k];
+      buf_load16_lds(w1 ? r1 : r2, off, dst + k * DX2_NT * 16);
+    }
+  };
+
+  // ---- X and dO rows in registers: B operand (lane = row b, 8 consecutive d) ----
+  u32x4 xr[KS], dr[KS];
+  {
+    const int b = b_wave + l32;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      u32x4 v = {0u, 0u, 0u, 0u}, w = {0u, 0u, 0u, 0u};
+      if (b < B) {
+        v = *(const u32x4*)(Xh + (size_t)b * D + ks * 16 + g * 8);
+        w = *(const u32x4*)(dOh + (size_t)b * D + ks * 16 + g * 8);
+      }
+      xr[ks] = v;
+      dr[ks] = w;
+    }
+  }
+
+  // ---- per-lane LDS offsets (slot relative) ----
+  // Z^T A operand (W1c^T), two transposed reads r = 0, 1: lane 4j + q of a 16-lane group
+  // reads row 16 ks + 8 g + 4 r + j, columns from 16 (G % 2) + 8 (q % 2) + 4 (q / 2);
+  // the row's swizzle is (2 g + r) & 3 for every ks.
+  unsigned offA[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r) {
+    const unsigned j = i16 >> 2, q = i16 & 3;
+    const unsigned chunk = 2u * (G & 1) + (q & 1u);
+    offA[r] = (8u * g + 4u * r + j) * 64u + ((chunk ^ ((2u * g + r) & 3u)) << 4) + 8u * (q >> 1);
+  }
+  // dH^T A operand: W2c row sig(l32), piece 2 ks + g -> offW2[ks % 2] + (ks / 2) * 2048
+  unsigned offW2[2];
+#pragma unroll
+  for (int kp = 0; kp < 2; ++kp) offW2[kp] = W2OFF + w2s_off(sig(l32), 2 * kp + g);
+  // dX B operand: W1c row 32 nt + l32, piece 2 s + g -> offB[s] + nt * 2048
+  unsigned offB[2];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) offB[s2] = l32 * 64u + (((2u * s2 + g) ^ ((l32 >> 2) & 3u)) << 4);
+
+  f32x16 acc[NTN];
+#pragma unroll
+  for (int nt = 0; nt < NTN; ++nt) acc[nt] = zero16();
+  f32x16 z = zero16(), dh = zero16();
+  u32x4 dz[2];
+
+  // MFMA phase over chunk c (G1: Z^T(c), dH^T(c)) and, when G2, chunk c - 1 (dX += dZ W1c^T)
+  auto mfma_phase = [&](auto G2, int c) {
+    constexpr bool DO_G2 = decltype(G2)::value;
+    constexpr int M2 = DO_G2 ? N2 : 0, NOPS = N1 + M2;
+    const int base1 = (c & 3) * (int)SLOT, base2 = ((c - 1) & 3) * (int)SLOT;
+    auto fetch = [&](int j) -> u32x4 {
+      const int q = sched_index(j, N1, M2);
+      if (sched_is_g2(j, N1, M2)) {
+        const int s2 = q / NTN, nt = q % NTN;
+        return lds_read16(base2 + (int)offB[s2] + nt * 2048);
+      }
+      const int ks = q >> 1;
+      if ((q & 1) == 0)
+        return cat(lds_read_tr(base1 + (int)offA[0] + ks * 1024), lds_read_tr(base1 + (int)offA[1] + ks * 1024));
+      return lds_read16(base1 + (int)offW2[ks & 1] + (ks >> 1) * 2048);
+    };
+    u32x4 ring[PD + 1];
+#pragma unroll
+    for (int j = 0; j < PD; ++j) ring[j] = fetch(j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NOPS; ++j) {
+      const u32x4 cur = ring[j % (PD + 1)];
+      if (j + PD < NOPS) ring[(j + PD) % (PD + 1)] = fetch(j + PD);
+      const int q = sched_index(j, N1, M2);
+      if (sched_is_g2(j, N1, M2)) {
+        const int s2 = q / NTN, nt = q % NTN;
+        acc[nt] = mfma<BF16>(dz[s2], cur, acc[nt]);
+      } else {
+        const int ks = q >> 1;  // ks == 0 starts the chain from a literal zero accumulator
+        if ((q & 1) == 0) z = mfma<BF16>(cur, xr[ks], ks == 0 ? zero16() : z);
+        else dh = mfma<BF16>(cur, dr[ks], ks == 0 ? zero16() : dh);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto g2_only = [&](int c) {  // dX += dZ(c) W1c(c)^T
+    const int base2 = (c & 3) * (int)SLOT;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) acc[nt] = mfma<BF16>(dz[s2], lds_read16(base2 + (int)offB[s2] + nt * 2048), acc[nt]);
+  };
+  auto valu_phase = [&]() {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+        dz[s2][w] = pack2<BF16>(act_b<ACT>(z[8 * s2 + 2 * w], dh[8 * s2 + 2 * w]),
+                                act_b<ACT>(z[8 * s2 + 2 * w + 1], dh[8 * s2 + 2 * w + 1]));
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // end of a chunk: this wave's DMA for chunk c + 1 has landed (the one for c + 2 may be in
+  // flight); the barrier publishes it and retires every read of the slot chunk c + 3 reuses
+  auto chunk_end = [&]() {
+    wait_vmcnt<NDMA>();
+    __builtin_amdgcn_s_barrier();
+  };
+
+  issue_chunk(0);
+  issue_chunk(1);
+  wait_vmcnt<NDMA>();
+  __builtin_amdgcn_s_barrier();
+  const std::true_type T{};
+  const std::false_type F{};
+  if (!late) {
+    issue_chunk(2);
+    mfma_phase(F, 0);
+    valu_phase();
+    chunk_end();
+    for (int c = 1; c < NC; ++c) {
+      issue_chunk(c + 2);
+      mfma_phase(T, c);
+      valu_phase();
+      chunk_end();
+    }
+  } else {
+    issue_chunk(2);
+    mfma_phase(F, 0);
+    chunk_end();
+    for (int c = 1; c < NC; ++c) {
+      issue_chunk(c + 2);
+      valu_phase();
+      mfma_phase(T, c);
+      chunk_end();
+    }
+    valu_phase();
+  }
+  g2_only(NC - 1);
+  wait_vmcnt<0>();  // no DMA may still target LDS when the workgroup ends
+
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int b = b_wave + 8 * (i >> 2) + 4 * g + (i & 3);
+    if (b < B) {
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) dXh[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(acc[nt][i]);
+    }
+  }
+}
+
 // dW programs: one wave per SIMD (the role keeps W1c^T / W2c fragments and both dW
 // accumulators in registers).
 template <bool BF16, int D, int ACT>
@@ -634,10 +864,12 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus) {
   p.rows_per_split = (int)rps;
   // dX programs: 256 rows when that still gives >= 2 programs per CU, else 128
   // (D = 128 with two M-tiles per wave exceeds the register file, so it keeps one)
-  const long long big = (B + 255) / 256 * H;
-  (void)big;
+  // dX programs: the 8-wave form unless it would leave most CUs idle (measured on MI355X:
+  // it wins from about a quarter of the CUs busy, the 4-wave form below that)
+  const long long big = (B + DX2_ROWS - 1) / DX2_ROWS * H;
   p.dx_mt = 1;
-  const int rows = dx_waves((int)D) * 32 * p.dx_mt;
+  p.dx_kind = env_int("FMLP_DX_KIND", 4 * big >= num_cus ? 1 : 0) ? 1 : 0;
+  const int rows = p.dx_kind ? DX2_ROWS : dx_waves((int)D) * 32 * p.dx_mt;
   p.dx_tiles_per_head = (int)((B + rows - 1) / rows);
   p.n_dw = base * p.nS;
   p.n_dx = (long long)p.dx_tiles_per_head * H;
@@ -679,8 +911,17 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
                          (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head);
       return hipGetLastError();
     };
-    if (D == 64 && p.dx_mt == 2) e = launch(dx_kernel<BF16, D, ACT, (D == 64 ? 2 : 1)>);
-    else e = launch(dx_kernel<BF16, D, ACT, 1>);
+    if (p.dx_kind == 1) {
+      const size_t lds2 = 4u * 128u * D;
+      auto k = dx2_kernel<BF16, D, ACT>;
+      e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(DX2_NT), lds2, st, (const u16*)a.x, (const u16*)a.w1,
+                         (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head);
+      e = hipGetLastError();
+    } else {
+      e = launch(dx_kernel<BF16, D, ACT, 1>);
+    }
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

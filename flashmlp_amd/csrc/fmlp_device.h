@@ -187,6 +187,36 @@ __device__ __forceinline__ u32x4 buf_load16(Rsrc r, unsigned byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
 }
 
+// 16 bytes per lane from a buffer straight into LDS (no registers): lane L's bytes land at
+// lds_byte_off + 16 L (lds_byte_off wave-uniform; verified on MI355X). Issued as inline
+// assembly on purpose: the compiler would otherwise treat every later LDS read as
+// possibly reading the in-flight DMA data and wait for all of it, which removes the
+// lookahead. Callers order DMA and reads themselves with wait_vmcnt<N>() (at most N
+// vector-memory operations of the wave outstanding) and a workgroup barrier. Loads
+// complete in issue order, so the compiler's own vmcnt waits stay correct (they can only
+// become stricter). The resource words are those of make_rsrc (stride 0, gfx9 format).
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 make_rsrc_words(const void* base, long long bytes) {
+  const unsigned long long a = (unsigned long long)base;
+  const int n = bytes <= 0 ? 0 : (bytes >= 0x7fffffffLL ? 0x7fffffff : (int)bytes);
+  i32x4 w = {__builtin_amdgcn_readfirstlane((int)(unsigned)a), __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffffu)),
+             __builtin_amdgcn_readfirstlane(n), 0x00020000};
+  return w;
+}
+__device__ __forceinline__ void buf_load16_lds(const i32x4& rsrc, unsigned byte_off, int lds_byte_off) {
+  const unsigned m0 = (unsigned)__builtin_amdgcn_readfirstlane(
+      (int)(unsigned)(uintptr_t)((FMLP_LDS char*)fmlp_lds + lds_byte_off));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+               :
+               : "v"(byte_off), "s"(rsrc), "s"(m0)
+               : "memory", "m0");
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8) | ((N >> 4) << 14));
+}
+
 // Row swizzle for row-major tiles whose rows are D 16-bit values (D = 64 or 128) and that
 // are read both row-wise (16-byte chunks, lane m reads row m) and with ds_read_b64_tr_b16
 // over 4-row x 32-byte blocks. 16-byte chunk c of row r is stored at chunk c ^ swz(r).
