@@ -578,8 +578,8 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
 // Waves 0-3 run MFMA-then-VALU, waves 4-7 VALU(c-1)-then-MFMA, so the two waves sharing a
 // SIMD keep the matrix cores and the VALU busy at the same time (the per-chunk barrier
 // would otherwise align them). Nothing is double-buffered in registers, which keeps a wave
-// within 256 VGPRs. W1c / W2c chunks go from memory straight into a 4-slot LDS ring
-// (buffer loads to LDS, two chunks ahead).
+// within 256 VGPRs. W1c / W2c chunks are staged through registers into a 4-slot LDS ring
+// (loaded one chunk ahead, stored at the start of the next chunk).
 //
 // E-order inside a chunk: Z^T row m holds chunk column e = sig(m) (bits 2 and 3 of m
 // swapped). Then the 8 k-slots a lane holds of the dZ operand (C layout rows
@@ -589,8 +589,8 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
 //
 // LDS slot (128 D bytes): W1c [D rows d][32 columns e] 64-byte rows, 16-byte chunk q of row
 // r at chunk q ^ ((r >> 2) & 3); then W2c [32 rows e][D] as D/32 blocks of [32][32]
-// (w2s_off). Both are written by lane-linear 16-byte DMA pieces; each lane loads the
-// global piece that belongs at its LDS position.
+// (w2s_off). Both are written as lane-linear 16-byte pieces; each lane loads the global
+// piece that belongs at its LDS position.
 // ------------------------------------------------------------------------------------
 __device__ __forceinline__ constexpr unsigned sig(unsigned m) {
   return (m & ~12u) | ((m & 4u) << 1) | ((m & 8u) >> 1);
@@ -607,7 +607,7 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr unsigned SLOT = 128u * D;
   constexpr unsigned W2OFF = 64u * D;
-  constexpr int NDMA = D / 64;  // 1 KB DMA instructions per wave per chunk
+  constexpr int NDMA = D / 64;  // 16-byte pieces per lane per chunk
   constexpr int N1 = 2 * KS, N2 = 2 * NTN;
   constexpr int PD = 3;
 
@@ -626,7 +626,7 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   u16* dXh = dX + (size_t)h * B * D;
   const int b_wave = bt * DX2_ROWS + wave * 32;
 
-  // ---- DMA pieces: piece p (16 bytes at slot offset 16 p) of a chunk ----
+  // ---- staging pieces: piece p (16 bytes at slot offset 16 p) of a chunk ----
   unsigned dmaOff[NDMA];
   int dmaCol[NDMA];  // W1c pieces: first chunk column (masked against E); W2c pieces: -1
 #pragma unroll
@@ -643,17 +643,23 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       dmaCol[k] = -1;
     }
   }
-  auto issue_chunk = [&](int c) {
+  // chunk staging: global -> registers (issued one iteration ahead) -> LDS
+  u32x4 stg[NDMA];
+  auto load_chunk = [&](int c) {
     const int lim = E - c * 32;
-    const i32x4 r1 = make_rsrc_words(W1h + (size_t)c * 32, (long long)D * E * 2 - 64LL * c);
-    const i32x4 r2 = make_rsrc_words(W2h + (size_t)c * 32 * D, (long long)min(max(lim, 0), 32) * D * 2);
-    const int dst = (c & 3) * (int)SLOT + wave * 1024;
+    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, (long long)D * E * 2 - 64LL * c);
+    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, (long long)min(max(lim, 0), 32) * D * 2);
 #pragma unroll
     for (int k = 0; k < NDMA; ++k) {
       const bool w1 = (unsigned)(k * DX2_NT + wave * 64) < 4u * D;  // wave-uniform
       const unsigned off = w1 ? (dmaCol[k] < lim ? dmaOff[k] : BUF_OOB) : dmaOff[k];
-      buf_load16_lds(w1 ? r1 : r2, off, dst + k * DX2_NT * 16);
+      stg[k] = buf_load16(w1 ? r1 : r2, off);
     }
+  };
+  auto store_chunk = [&](int c) {
+    const int dst = (c & 3) * (int)SLOT + wave * 1024 + lane * 16;
+#pragma unroll
+    for (int k = 0; k < NDMA; ++k) lds_write16(dst + k * DX2_NT * 16, stg[k]);
   };
 
   // ---- X and dO rows in registers: B operand (lane = row b, 8 consecutive d) ----
@@ -750,36 +756,43 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
                                 act_b<ACT>(z[8 * s2 + 2 * w + 1], dh[8 * s2 + 2 * w + 1]));
     __builtin_amdgcn_sched_barrier(0);
   };
-  // end of a chunk: this wave's DMA for chunk c + 1 has landed (the one for c + 2 may be in
-  // flight); the barrier publishes it and retires every read of the slot chunk c + 3 reuses
+  // iteration c stores chunk c + 1 (loaded during iteration c - 1) into its slot and loads
+  // chunk c + 2; the end-of-chunk barrier publishes the stores (their LDS writes retired)
+  // and retires every read of the slot they reuse
+  auto chunk_begin = [&](int c) {
+    store_chunk(c + 1);
+    load_chunk(c + 2);
+  };
   auto chunk_end = [&]() {
-    wait_vmcnt<NDMA>();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");       // keep LDS accesses on their side of the barrier
     __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   };
 
-  issue_chunk(0);
-  issue_chunk(1);
-  wait_vmcnt<NDMA>();
-  __builtin_amdgcn_s_barrier();
+  load_chunk(0);
+  store_chunk(0);
+  load_chunk(1);
+  chunk_end();
   const std::true_type T{};
   const std::false_type F{};
   if (!late) {
-    issue_chunk(2);
+    chunk_begin(0);
     mfma_phase(F, 0);
     valu_phase();
     chunk_end();
     for (int c = 1; c < NC; ++c) {
-      issue_chunk(c + 2);
+      chunk_begin(c);
       mfma_phase(T, c);
       valu_phase();
       chunk_end();
     }
   } else {
-    issue_chunk(2);
+    chunk_begin(0);
     mfma_phase(F, 0);
     chunk_end();
     for (int c = 1; c < NC; ++c) {
-      issue_chunk(c + 2);
+      chunk_begin(c);
       valu_phase();
       mfma_phase(T, c);
       chunk_end();
@@ -787,7 +800,6 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     valu_phase();
   }
   g2_only(NC - 1);
-  wait_vmcnt<0>();  // no DMA may still target LDS when the workgroup ends
 
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
