@@ -27,6 +27,51 @@ constexpr int DW_BT = 32;            // rows per streamed subtile
 // dX workgroups: 4 waves (128 rows).
 __host__ __device__ constexpr int dx_waves(int D) { return D > 0 ? 4 : 4; }
 
+// dW epilogue shared by the dW kernels. C layout of the accumulators: lane = column d
+// (32 nt + l32), rows e = e0 + 8 (i / 4) + 4 g + (i % 4). nS == 1 writes dW1, dW2 in the io
+// dtype; otherwise fp32 partials ws2[s][h][e][d] and ws1[s][h][e][d] (= dW1^T) for
+// dw_reduce_kernel.
+template <bool BF16, int D>
+__device__ __forceinline__ void dw_store(const f32x16 (&a1)[D / 32], const f32x16 (&a2)[D / 32], u16* __restrict__ dW1,
+                                         u16* __restrict__ dW2, float* __restrict__ ws, int H, int E, int h, int s,
+                                         int nS, int e0, int g, int l32) {
+  constexpr int NTN = D / 32;
+  if (nS == 1) {
+    u16* dW2h = dW2 + (size_t)h * E * D;
+    u16* dW1h = dW1 + (size_t)h * D * E;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int eb = e0 + 8 * i4 + 4 * g;  // 4 consecutive columns eb .. eb+3 (E % 8 == 0)
+      if (eb < E) {
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) {
+          const int d = nt * 32 + l32;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dW2h[(size_t)(eb + j) * D + d] = from_f32<BF16>(a2[nt][4 * i4 + j]);
+          u32x2 v = {pack2<BF16>(a1[nt][4 * i4 + 0], a1[nt][4 * i4 + 1]), pack2<BF16>(a1[nt][4 * i4 + 2], a1[nt][4 * i4 + 3])};
+          *(u32x2*)(dW1h + (size_t)d * E + eb) = v;
+        }
+      }
+    }
+  } else {
+    const size_t per = (size_t)H * E * D;
+    float* p2 = ws + ((size_t)s * H + h) * E * D;
+    float* p1 = ws + (size_t)nS * per + ((size_t)s * H + h) * E * D;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int e = e0 + 8 * (i >> 2) + 4 * g + (i & 3);
+      if (e < E) {
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) {
+          const int d = nt * 32 + l32;
+          p2[(size_t)e * D + d] = a2[nt][i];
+          p1[(size_t)e * D + d] = a1[nt][i];
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------
 // dW role
 // ------------------------------------------------------------------------------------
@@ -274,42 +319,7 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
     }
   }
 
-  // ---- epilogue. C layout: lane = column d (32nt + l32), rows e = 8(i/4) + 4g + (i%4) ----
-  if (nS == 1) {
-    u16* dW2h = dW2 + (size_t)h * E * D;
-    u16* dW1h = dW1 + (size_t)h * D * E;
-#pragma unroll
-    for (int i4 = 0; i4 < 4; ++i4) {
-      const int eb = e0 + 8 * i4 + 4 * g;  // 4 consecutive columns eb .. eb+3 (E % 8 == 0)
-      if (eb < E) {
-#pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) {
-          const int d = nt * 32 + l32;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) dW2h[(size_t)(eb + j) * D + d] = from_f32<BF16>(a2[nt][4 * i4 + j]);
-          u32x2 v = {pack2<BF16>(a1[nt][4 * i4 + 0], a1[nt][4 * i4 + 1]), pack2<BF16>(a1[nt][4 * i4 + 2], a1[nt][4 * i4 + 3])};
-          *(u32x2*)(dW1h + (size_t)d * E + eb) = v;
-        }
-      }
-    }
-  } else {
-    // fp32 partials, both in (e, d) layout: ws2[s][h][e][d], ws1[s][h][e][d] (= dW1^T)
-    const size_t per = (size_t)H * E * D;
-    float* p2 = ws + ((size_t)s * H + h) * E * D;
-    float* p1 = ws + (size_t)nS * per + ((size_t)s * H + h) * E * D;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int e = e0 + 8 * (i >> 2) + 4 * g + (i & 3);
-      if (e < E) {
-#pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) {
-          const int d = nt * 32 + l32;
-          p2[(size_t)e * D + d] = a2[nt][i];
-          p1[(size_t)e * D + d] = a1[nt][i];
-        }
-      }
-    }
-  }
+  dw_store<BF16, D>(a1, a2, dW1, dW2, ws, H, E, h, s, nS, e0, g, l32);
 }
 
 // ------------------------------------------------------------------------------------
@@ -811,6 +821,282 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   }
 }
 
+// ------------------------------------------------------------------------------------
+// dW programs, two-waves-per-SIMD form (dw2_kernel): 8 waves per (head, 128-column E-tile,
+// B-range). Waves w and w + 4 share a SIMD and the E-columns 32 (w % 4) .. + 31 and take
+// alternate 32-row subtiles (set 0 = waves 0-3 the even ones, set 1 the odd ones); their
+// dW partial sums are added through LDS at the end. The E-tile's W1c^T and W2c are kept
+// in LDS (no room in registers next to both dW accumulators), so every Z / dH MFMA reads
+// both operands from LDS:
+//   W1T [128 e][D] and W2T [128 e][D] : D/32 blocks of [128 rows][64 bytes], 16-byte chunk
+//       q of row r at chunk q ^ ((r >> 2) & 3) (wt_off), read row-wise (lane = column e);
+//   ring of 3 slots, each a subtile pair [X set0][dO set0][X set1][dO set1] of [32][D]
+//       in the w2s_off layout, written by lane-linear buffer-to-LDS loads one pair ahead.
+// Per pair each wave runs an MFMA phase (Z, dH of its subtile: 16 MFMAs, interleaved with
+// dW2 += h^T dO and dW1^T += dZ^T X of its previous subtile: 16 MFMAs) and a VALU phase
+// (h, dZ of the subtile); set 0 runs MFMA-then-VALU and set 1 VALU(previous)-then-MFMA so
+// that the two waves of a SIMD are in opposite phases.
+// ------------------------------------------------------------------------------------
+constexpr int DW2_NW = 8;
+constexpr int DW2_NT = DW2_NW * 64;
+
+__device__ __forceinline__ unsigned wt_off(unsigned r, unsigned q) {
+  return (q >> 2) * 8192u + r * 64u + (((q & 3u) ^ ((r >> 2) & 3u)) << 4);
+}
+
+template <bool BF16, int D, int ACT>
+__global__ void __launch_bounds__(DW2_NT)
+dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+           const u16* __restrict__ dO, u16* __restrict__ dW1, u16* __restrict__ dW2, float* __restrict__ ws,
+           int H, int B, int E, int nE, int nS, int rows_per_split) {
+  constexpr int KS = D / 16, NTN = D / 32;
+  constexpr int SUB = 64 * D;            // bytes of a [32][D] subtile
+  constexpr int PAIR = 4 * SUB;          // X set0, dO set0, X set1, dO set1
+  constexpr int WT = 256 * D;            // bytes of a [128][D] weight tile
+  constexpr int W2T_OFF = WT, RING_OFF = 2 * WT;
+  constexpr int NPL = PAIR / 16 / DW2_NT;  // 16-byte pieces per lane per pair
+  constexpr int N1 = 2 * KS, N2 = 4 * NTN;
+  constexpr int PD = 2;
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
+  const int cg = wave & 3, set = wave >> 2;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int et = t % nE;
+  const int hs = t / nE;
+  const int s = hs % nS, h = hs / nS;
+  const int e_prog = et * DW_ET;
+  const int e0 = e_prog + 32 * cg;
+  const int b_lo = s * rows_per_split;
+  const int b_hi = min(B, b_lo + rows_per_split);
+  const int nsub = (b_hi - b_lo + DW_BT - 1) / DW_BT;
+  const int npair = (nsub + 1) >> 1;
+
+  const u16* Xh = X + (size_t)h * B * D;
+  const u16* dOh = dO + (size_t)h * B * D;
+  const u16* W1h = W1 + (size_t)h * D * E;
+  const u16* W2h = W2 + (size_t)h * E * D;
+
+  // ---- weight tiles (once): W2T rows natural, W1T transposed with 2-byte writes ----
+#pragma unroll
+  for (int k = 0; k < D / 32; ++k) {
+    const int p = tid + k * DW2_NT;
+    {  // W2 row e_prog + r, piece q
+      const int r = p / (D / 8), q = p % (D / 8);
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (e_prog + r < E) v = *(const u32x4*)(W2h + (size_t)(e_prog + r) * D + q * 8);
+      lds_write16(W2T_OFF + (int)wt_off(r, q), v);
+    }
+    {  // W1 row d, columns e_prog + 8u .. + 7  ->  W1T rows 8u + j, column d
+      const int d = p >> 4, u = p & 15;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (e_prog + 8 * u < E) v = *(const u32x4*)(W1h + (size_t)d * E + e_prog + 8 * u);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const u16 x = (u16)(v[j >> 1] >> (16 * (j & 1)));
+        *(FMLP_LDS u16*)((FMLP_LDS char*)fmlp_lds + wt_off(8 * u + j, d >> 3) + (d & 7) * 2) = x;
+      }
+    }
+  }
+
+  // ---- subtile pairs: lane-linear buffer-to-LDS pieces ----
+  unsigned pieceOff[NPL];
+#pragma unroll
+  for (int k = 0; k < NPL; ++k) {
+    const unsigned p = k * DW2_NT + wave * 64 + lane, pr = p % (SUB / 16), o = 16u * pr;
+    const unsigned r = (o % 2048u) / 64u, q = 4u * (o / 2048u) + (((o / 16u) & 3u) ^ ((r >> 2) & 3u));
+    pieceOff[k] = r * (D * 2u) + q * 16u;
+  }
+  auto issue_pair = [&](int i, int slot) {
+#pragma unroll
+    for (int k = 0; k < NPL; ++k) {
+      const int region = (k * DW2_NT + wave * 64) / (SUB / 16);  // wave-uniform: 0 X0, 1 dO0, 2 X1, 3 dO1
+      const int r0 = b_lo + (2 * i + (region >> 1)) * DW_BT;
+      const long long bytes = (long long)min(max(b_hi - r0, 0), DW_BT) * D * 2;
+      const i32x4 rs = make_rsrc_words(((region & 1) ? dOh : Xh) + (size_t)r0 * D, bytes);
+      buf_load16_lds(rs, pieceOff[k], RING_OFF + slot * PAIR + 16 * (k * DW2_NT + wave * 64));
+    }
+  };
+
+  // ---- per-lane LDS offsets ----
+  const int own = set * 2 * SUB;  // this wave's subtile inside a pair: X at own, dO at own + SUB
+  //   A operand of Z / dH: subtile row l32, piece 2 ks + g -> offRow[ks % 2] + (ks / 2) * 2048
+  int offRow[2];
+#pragma unroll
+  for (int kp = 0; kp < 2; ++kp) offRow[kp] = own + (int)w2s_off(l32, 2 * kp + g);
+  //   B operand of Z / dH: weight-tile row 32 cg + l32, piece 2 ks + g -> offWt[ks % 2] + (ks / 2) * 8192
+  int offWt[2];
+#pragma unroll
+  for (int kp = 0; kp < 2; ++kp) offWt[kp] = (int)wt_off(32 * cg + l32, 2 * kp + g);
+  //   B operand of dW2 / dW1^T (transposed subtile reads) -> offTr[r] + nt * 2048 + s * 1024
+  int offTr[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    offTr[r] = own + (int)(w2s_off(8 * r + 4 * g + (i16 >> 2), 2 * (G & 1) + ((i16 & 3) >> 1)) + 8u * (i16 & 1));
+
+  f32x16 a2[NTN], a1[NTN];
+#pragma unroll
+  for (int nt = 0; nt < NTN; ++nt) {
+    a2[nt] = zero16();
+    a1[nt] = zero16();
+  }
+  f32x16 z = zero16(), dh = zero16();
+  u32x4 hT[2], dzT[2];
+
+  struct Opnd {
+    u32x4 a, b;
+  };
+  // MFMA phase: Z, dH of the subtile in slot `cur` (group 1) and, when G2, dW2 / dW1^T over
+  // the previous subtile in slot `prev` (group 2)
+  auto mfma_phase = [&](auto G2, int cur, int prev) {
+    constexpr bool DO_G2 = decltype(G2)::value;
+    constexpr int M2 = DO_G2 ? N2 : 0, NOPS = N1 + M2;
+    const int base1 = RING_OFF + cur * PAIR, base2 = RING_OFF + prev * PAIR;
+    auto fetch = [&](int j) -> Opnd {
+      const int q = sched_index(j, N1, M2);
+      Opnd o;
+      if (sched_is_g2(j, N1, M2)) {  // (s, nt, which): which 0 -> dW2 (B = dO^T), 1 -> dW1^T (B = X^T)
+        const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1, which = q & 1;
+        const int bb = base2 + (which == 0 ? SUB : 0) + nt * 2048 + s2 * 1024;
+        o.a = cat(lds_read_tr(bb + offTr[0]), lds_read_tr(bb + offTr[1]));
+        o.b = o.a;
+        return o;
+      }
+      const int ks = q >> 1, which = q & 1;  // which 0 -> Z (X, W1T), 1 -> dH (dO, W2T)
+      o.a = lds_read16(base1 + (which ? SUB : 0) + offRow[ks & 1] + (ks >> 1) * 2048);
+      o.b = lds_read16((which ? W2T_OFF : 0) + offWt[ks & 1] + (ks >> 1) * 8192);
+      return o;
+    };
+    Opnd ring[PD + 1];
+#pragma unroll
+    for (int j = 0; j < PD; ++j) ring[j] = fetch(j);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NOPS; ++j) {
+      const Opnd cur_op = ring[j % (PD + 1)];
+      if (j + PD < NOPS) ring[(j + PD) % (PD + 1)] = fetch(j + PD);
+      const int q = sched_index(j, N1, M2);
+      if (sched_is_g2(j, N1, M2)) {
+        const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1;
+        if ((q & 1) == 0) a2[nt] = mfma<BF16>(hT[s2], cur_op.a, a2[nt]);
+        else a1[nt] = mfma<BF16>(dzT[s2], cur_op.a, a1[nt]);
+      } else {
+        const int ks = q >> 1;  // ks == 0 starts the chain from a literal zero accumulator
+        if ((q & 1) == 0) z = mfma<BF16>(cur_op.a, cur_op.b, ks == 0 ? zero16() : z);
+        else dh = mfma<BF16>(cur_op.a, cur_op.b, ks == 0 ? zero16() : dh);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  auto g2_only = [&](int prev) {
+    const int base2 = RING_OFF + prev * PAIR;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) {
+        const int bb = base2 + nt * 2048 + s2 * 1024;
+        a2[nt] = mfma<BF16>(hT[s2], cat(lds_read_tr(bb + SUB + offTr[0]), lds_read_tr(bb + SUB + offTr[1])), a2[nt]);
+        a1[nt] = mfma<BF16>(dzT[s2], cat(lds_read_tr(bb + offTr[0]), lds_read_tr(bb + offTr[1])), a1[nt]);
+      }
+  };
+  auto valu_phase = [&]() {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        float h0, d0, h1, d1;
+        act_fb<ACT>(z[8 * s2 + 2 * w], dh[8 * s2 + 2 * w], h0, d0);
+        act_fb<ACT>(z[8 * s2 + 2 * w + 1], dh[8 * s2 + 2 * w + 1], h1, d1);
+        hT[s2][w] = pack2<BF16>(h0, h1);
+        dzT[s2][w] = pack2<BF16>(d0, d1);
+      }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  // end of a pair: this wave's loads of the next pair have landed; the barrier publishes
+  // them and retires every read of the slot the pair after reuses
+  auto pair_end = [&]() {
+    wait_vmcnt<0>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  if (npair > 0) {
+    issue_pair(0, 0);
+    pair_end();  // also publishes the weight tiles
+    const std::true_type T{};
+    const std::false_type F{};
+    int cur = 0, prev = 2, next = 1;  // ring slots of pairs i, i - 1, i + 1
+    auto rotate = [&]() {
+      const int tmp = prev;
+      prev = cur;
+      cur = next;
+      next = tmp;
+    };
+    issue_pair(1, next);
+    mfma_phase(F, cur, prev);
+    if (set == 0) {
+      valu_phase();
+      pair_end();
+      for (int i = 1; i < npair; ++i) {
+        rotate();
+        issue_pair(i + 1, next);
+        mfma_phase(T, cur, prev);
+        valu_phase();
+        pair_end();
+      }
+    } else {
+      pair_end();
+      for (int i = 1; i < npair; ++i) {
+        rotate();
+        issue_pair(i + 1, next);
+        valu_phase();
+        mfma_phase(T, cur, prev);
+        pair_end();
+      }
+      valu_phase();
+    }
+    g2_only(cur);
+  } else {
+    wait_vmcnt<0>();
+  }
+
+  // ---- add the two sets' partial sums through LDS (set 1 writes, set 0 adds) ----
+  asm volatile("" ::: "memory");
+  __syncthreads();
+  {
+    const int xb = cg * (2 * NTN * 16 * 256);  // 2 NTN accumulators x 16 registers x 64 lanes x 4 bytes
+    if (set == 1) {
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          u32x4 v2 = {__float_as_uint(a2[nt][4 * i4]), __float_as_uint(a2[nt][4 * i4 + 1]), __float_as_uint(a2[nt][4 * i4 + 2]), __float_as_uint(a2[nt][4 * i4 + 3])};
+          u32x4 v1 = {__float_as_uint(a1[nt][4 * i4]), __float_as_uint(a1[nt][4 * i4 + 1]), __float_as_uint(a1[nt][4 * i4 + 2]), __float_as_uint(a1[nt][4 * i4 + 3])};
+          lds_write16(xb + ((nt * 4 + i4) * 64 + lane) * 16, v2);
+          lds_write16(xb + (((NTN + nt) * 4 + i4) * 64 + lane) * 16, v1);
+        }
+    }
+    __syncthreads();
+    if (set == 0) {
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const u32x4 v2 = lds_read16(xb + ((nt * 4 + i4) * 64 + lane) * 16);
+          const u32x4 v1 = lds_read16(xb + (((NTN + nt) * 4 + i4) * 64 + lane) * 16);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            a2[nt][4 * i4 + j] += __uint_as_float(v2[j]);
+            a1[nt][4 * i4 + j] += __uint_as_float(v1[j]);
+          }
+        }
+      dw_store<BF16, D>(a1, a2, dW1, dW2, ws, H, E, h, s, nS, e0, g, l32);
+    }
+  }
+}
+
 // dW programs: one wave per SIMD (the role keeps W1c^T / W2c fragments and both dW
 // accumulators in registers).
 template <bool BF16, int D, int ACT>
@@ -874,6 +1160,7 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus) {
   if (ns < 1) ns = 1;
   p.nS = (int)ns;
   p.rows_per_split = (int)rps;
+  p.dw_kind = env_int("FMLP_DW_KIND", 1) ? 1 : 0;
   // dX programs: 256 rows when that still gives >= 2 programs per CU, else 128
   // (D = 128 with two M-tiles per wave exceeds the register file, so it keeps one)
   // dX programs: the 8-wave form unless it would leave most CUs idle (measured on MI355X:
@@ -895,13 +1182,23 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   hipError_t e;
   // dW programs (and their partial reduction), then dX programs, in stream order
   if (p.n_dw > 0) {
-    const size_t lds = 4u * 128u * D > (size_t)D * DW_ET * 2 ? 4u * 128u * D : (size_t)D * DW_ET * 2;
-    auto k = dw_kernel<BF16, D, ACT>;
-    e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(BWD_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                       (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws, (int)a.H,
-                       (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split);
+    if (p.dw_kind == 1) {
+      const size_t lds = 1280u * D;  // two weight tiles (256 D each) + three subtile pairs (256 D each)
+      auto k = dw2_kernel<BF16, D, ACT>;
+      e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                         (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws, (int)a.H,
+                         (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split);
+    } else {
+      const size_t lds = 4u * 128u * D > (size_t)D * DW_ET * 2 ? 4u * 128u * D : (size_t)D * DW_ET * 2;
+      auto k = dw_kernel<BF16, D, ACT>;
+      e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(BWD_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                         (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws, (int)a.H,
+                         (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split);
+    }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (p.nS > 1) {

@@ -29,6 +29,7 @@ struct BwdPlan {
   int rows_per_split;  // multiple of 32
   int dx_mt;           // 32-row M-tiles per wave in dX programs (rows per program = 128 * dx_mt)
   int dx_kind;         // 0: 4-wave software-pipelined dX programs (128 rows); 1: 8-wave (256 rows)
+  int dw_kind;         // 0: 4-wave dW programs (one wave per SIMD); 1: 8-wave (two per SIMD)
   int dx_tiles_per_head;
   long long n_dw, n_dx;
   size_t ws_bytes;     // fp32 partials when nS > 1
