@@ -147,7 +147,7 @@ __device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __
   }
   auto load_sub = [&](int k) {
     const int r0 = b_lo + k * DW_BT;
-    const long long bytes = (long long)min(max(b_hi - r0, 0), DW_BT) * D * 2;
+    const int bytes = clamp0(b_hi - r0, DW_BT) * D * 2;
     const Rsrc rx = make_rsrc(Xh + (size_t)r0 * D, bytes);
     const Rsrc rd = make_rsrc(dOh + (size_t)r0 * D, bytes);
 #pragma unroll
@@ -363,8 +363,8 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
   }
   auto load_chunk = [&](int c) {
     const int lim = E - c * 32;
-    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, (long long)D * E * 2 - 64LL * c);
-    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, (long long)min(max(lim, 0), 32) * D * 2);
+    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, D * E * 2 - 64 * c);
+    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
 #pragma unroll
     for (int k = 0; k < PPT / 2; ++k) {
       stg[k] = buf_load16(r1, (int)colq < lim ? offW1g[k] : BUF_OOB);
@@ -657,8 +657,8 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   u32x4 stg[NDMA];
   auto load_chunk = [&](int c) {
     const int lim = E - c * 32;
-    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, (long long)D * E * 2 - 64LL * c);
-    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, (long long)min(max(lim, 0), 32) * D * 2);
+    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, D * E * 2 - 64 * c);
+    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
 #pragma unroll
     for (int k = 0; k < NDMA; ++k) {
       const bool w1 = (unsigned)(k * DX2_NT + wave * 64) < 4u * D;  // wave-uniform
@@ -832,10 +832,10 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 //       q of row r at chunk q ^ ((r >> 2) & 3) (wt_off), read row-wise (lane = column e);
 //   ring of 3 slots, each a subtile pair [X set0][dO set0][X set1][dO set1] of [32][D]
 //       in the w2s_off layout, written by lane-linear buffer-to-LDS loads one pair ahead.
-// Per pair each wave runs an MFMA phase (Z, dH of its subtile: 16 MFMAs, interleaved with
-// dW2 += h^T dO and dW1^T += dZ^T X of its previous subtile: 16 MFMAs) and a VALU phase
-// (h, dZ of the subtile); set 0 runs MFMA-then-VALU and set 1 VALU(previous)-then-MFMA so
-// that the two waves of a SIMD are in opposite phases.
+// Per pair each wave computes Z, dH of its subtile (16 MFMAs), then h, dZ interleaved with
+// dW2 += h^T dO and dW1^T += dZ^T X over the same subtile (16 MFMAs); set 0 does this for
+// the current pair, set 1 finishes the previous pair first, so the two waves of a SIMD
+// are half a pair apart.
 // ------------------------------------------------------------------------------------
 constexpr int DW2_NW = 8;
 constexpr int DW2_NT = DW2_NW * 64;
@@ -853,7 +853,10 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   constexpr int SUB = 64 * D;            // bytes of a [32][D] subtile
   constexpr int PAIR = 4 * SUB;          // X set0, dO set0, X set1, dO set1
   constexpr int WT = 256 * D;            // bytes of a [128][D] weight tile
-  constexpr int W2T_OFF = WT, RING_OFF = 2 * WT;
+  // ring first (its runtime slot base plus constant offsets stays within the 16-bit DS
+  // immediate range), weight tiles above it (addressed from a lane register that holds
+  // the tile base)
+  constexpr int RING_OFF = 0, W1T_OFF = 3 * PAIR, W2T_OFF = W1T_OFF + WT;
   constexpr int NPL = PAIR / 16 / DW2_NT;  // 16-byte pieces per lane per pair
   constexpr int N1 = 2 * KS, N2 = 4 * NTN;
   constexpr int PD = 2;
@@ -895,7 +898,7 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const u16 x = (u16)(v[j >> 1] >> (16 * (j & 1)));
-        *(FMLP_LDS u16*)((FMLP_LDS char*)fmlp_lds + wt_off(8 * u + j, d >> 3) + (d & 7) * 2) = x;
+        *(FMLP_LDS u16*)((FMLP_LDS char*)fmlp_lds + W1T_OFF + wt_off(8 * u + j, d >> 3) + (d & 7) * 2) = x;
       }
     }
   }
@@ -913,7 +916,7 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     for (int k = 0; k < NPL; ++k) {
       const int region = (k * DW2_NT + wave * 64) / (SUB / 16);  // wave-uniform: 0 X0, 1 dO0, 2 X1, 3 dO1
       const int r0 = b_lo + (2 * i + (region >> 1)) * DW_BT;
-      const long long bytes = (long long)min(max(b_hi - r0, 0), DW_BT) * D * 2;
+      const int bytes = clamp0(b_hi - r0, DW_BT) * D * 2;
       const i32x4 rs = make_rsrc_words(((region & 1) ? dOh : Xh) + (size_t)r0 * D, bytes);
       buf_load16_lds(rs, pieceOff[k], RING_OFF + slot * PAIR + 16 * (k * DW2_NT + wave * 64));
     }
@@ -928,7 +931,7 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   //   B operand of Z / dH: weight-tile row 32 cg + l32, piece 2 ks + g -> offWt[ks % 2] + (ks / 2) * 8192
   int offWt[2];
 #pragma unroll
-  for (int kp = 0; kp < 2; ++kp) offWt[kp] = (int)wt_off(32 * cg + l32, 2 * kp + g);
+  for (int kp = 0; kp < 2; ++kp) offWt[kp] = W1T_OFF + (int)wt_off(32 * cg + l32, 2 * kp + g);
   //   B operand of dW2 / dW1^T (transposed subtile reads) -> offTr[r] + nt * 2048 + s * 1024
   int offTr[2];
 #pragma unroll
@@ -947,25 +950,15 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   struct Opnd {
     u32x4 a, b;
   };
-  // MFMA phase: Z, dH of the subtile in slot `cur` (group 1) and, when G2, dW2 / dW1^T over
-  // the previous subtile in slot `prev` (group 2)
-  auto mfma_phase = [&](auto G2, int cur, int prev) {
-    constexpr bool DO_G2 = decltype(G2)::value;
-    constexpr int M2 = DO_G2 ? N2 : 0, NOPS = N1 + M2;
-    const int base1 = RING_OFF + cur * PAIR, base2 = RING_OFF + prev * PAIR;
-    auto fetch = [&](int j) -> Opnd {
-      const int q = sched_index(j, N1, M2);
-      Opnd o;
-      if (sched_is_g2(j, N1, M2)) {  // (s, nt, which): which 0 -> dW2 (B = dO^T), 1 -> dW1^T (B = X^T)
-        const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1, which = q & 1;
-        const int bb = base2 + (which == 0 ? SUB : 0) + nt * 2048 + s2 * 1024;
-        o.a = cat(lds_read_tr(bb + offTr[0]), lds_read_tr(bb + offTr[1]));
-        o.b = o.a;
-        return o;
-      }
+  // Z and dH of the wave's subtile of the pair in `slot`: 16 MFMAs, both operands from LDS,
+  // read PD steps ahead
+  auto g1_phase = [&](int slot) {
+    const int base = RING_OFF + slot * PAIR;
+    auto fetch = [&](int q) -> Opnd {
       const int ks = q >> 1, which = q & 1;  // which 0 -> Z (X, W1T), 1 -> dH (dO, W2T)
-      o.a = lds_read16(base1 + (which ? SUB : 0) + offRow[ks & 1] + (ks >> 1) * 2048);
-      o.b = lds_read16((which ? W2T_OFF : 0) + offWt[ks & 1] + (ks >> 1) * 8192);
+      Opnd o;
+      o.a = lds_read16(base + (which ? SUB : 0) + offRow[ks & 1] + (ks >> 1) * 2048);
+      o.b = lds_read16((which ? WT : 0) + offWt[ks & 1] + (ks >> 1) * 8192);
       return o;
     };
     Opnd ring[PD + 1];
@@ -973,45 +966,52 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     for (int j = 0; j < PD; ++j) ring[j] = fetch(j);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 0; j < NOPS; ++j) {
-      const Opnd cur_op = ring[j % (PD + 1)];
-      if (j + PD < NOPS) ring[(j + PD) % (PD + 1)] = fetch(j + PD);
-      const int q = sched_index(j, N1, M2);
-      if (sched_is_g2(j, N1, M2)) {
-        const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1;
-        if ((q & 1) == 0) a2[nt] = mfma<BF16>(hT[s2], cur_op.a, a2[nt]);
-        else a1[nt] = mfma<BF16>(dzT[s2], cur_op.a, a1[nt]);
-      } else {
-        const int ks = q >> 1;  // ks == 0 starts the chain from a literal zero accumulator
-        if ((q & 1) == 0) z = mfma<BF16>(cur_op.a, cur_op.b, ks == 0 ? zero16() : z);
-        else dh = mfma<BF16>(cur_op.a, cur_op.b, ks == 0 ? zero16() : dh);
-      }
+    for (int q = 0; q < N1; ++q) {
+      const Opnd cur_op = ring[q % (PD + 1)];
+      if (q + PD < N1) ring[(q + PD) % (PD + 1)] = fetch(q + PD);
+      const int ks = q >> 1;  // ks == 0 starts the chain from a literal zero accumulator
+      if ((q & 1) == 0) z = mfma<BF16>(cur_op.a, cur_op.b, ks == 0 ? zero16() : z);
+      else dh = mfma<BF16>(cur_op.a, cur_op.b, ks == 0 ? zero16() : dh);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  auto g2_only = [&](int prev) {
-    const int base2 = RING_OFF + prev * PAIR;
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) {
-        const int bb = base2 + nt * 2048 + s2 * 1024;
-        a2[nt] = mfma<BF16>(hT[s2], cat(lds_read_tr(bb + SUB + offTr[0]), lds_read_tr(bb + SUB + offTr[1])), a2[nt]);
-        a1[nt] = mfma<BF16>(dzT[s2], cat(lds_read_tr(bb + offTr[0]), lds_read_tr(bb + offTr[1])), a1[nt]);
+  // h, dZ of the subtile whose Z, dH are in registers, and dW2 += h^T dO, dW1^T += dZ^T X
+  // over it (its pair is in `slot`). Elements 0-7 (the K-step-0 operands) are activated
+  // first; the 8 K-step-0 MFMAs then run with elements 8-15 spread between them, and the
+  // 8 K-step-1 MFMAs follow.
+  auto ag2_phase = [&](int slot) {
+    const int base2 = RING_OFF + slot * PAIR;
+    auto fetch = [&](int q) -> u32x4 {  // (s, nt, which): which 0 -> dW2 (B = dO^T), 1 -> dW1^T (B = X^T)
+      const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1, which = q & 1;
+      const int bb = base2 + (which == 0 ? SUB : 0) + nt * 2048 + s2 * 1024;
+      return cat(lds_read_tr(bb + offTr[0]), lds_read_tr(bb + offTr[1]));
+    };
+    auto act_elem = [&](int e, float (&hv)[16], float (&dv)[16]) {
+      act_fb<ACT>(z[e], dh[e], hv[e], dv[e]);
+      if (e & 1) {
+        hT[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1], hv[e]);
+        dzT[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
       }
-  };
-  auto valu_phase = [&]() {
+    };
+    float hv[16], dv[16];
+    u32x4 ring[PD + 1];
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
+    for (int j = 0; j < PD; ++j) ring[j] = fetch(j);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        float h0, d0, h1, d1;
-        act_fb<ACT>(z[8 * s2 + 2 * w], dh[8 * s2 + 2 * w], h0, d0);
-        act_fb<ACT>(z[8 * s2 + 2 * w + 1], dh[8 * s2 + 2 * w + 1], h1, d1);
-        hT[s2][w] = pack2<BF16>(h0, h1);
-        dzT[s2][w] = pack2<BF16>(d0, d1);
-      }
+    for (int e = 0; e < 8; ++e) act_elem(e, hv, dv);
     __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int q = 0; q < N2; ++q) {
+      const u32x4 cur_op = ring[q % (PD + 1)];
+      if (q + PD < N2) ring[(q + PD) % (PD + 1)] = fetch(q + PD);
+      const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1;
+      if ((q & 1) == 0) a2[nt] = mfma<BF16>(hT[s2], cur_op, a2[nt]);
+      else a1[nt] = mfma<BF16>(dzT[s2], cur_op, a1[nt]);
+#pragma unroll
+      for (int e = 8 + sched_elem_begin(q, N2 / 2, 8); e < 8 + sched_elem_begin(q + 1, N2 / 2, 8); ++e)
+        if (e < 16) act_elem(e, hv, dv);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
   // end of a pair: this wave's loads of the next pair have landed; the barrier publishes
   // them and retires every read of the slot the pair after reuses
@@ -1025,8 +1025,6 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   if (npair > 0) {
     issue_pair(0, 0);
     pair_end();  // also publishes the weight tiles
-    const std::true_type T{};
-    const std::false_type F{};
     int cur = 0, prev = 2, next = 1;  // ring slots of pairs i, i - 1, i + 1
     auto rotate = [&]() {
       const int tmp = prev;
@@ -1035,15 +1033,15 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       next = tmp;
     };
     issue_pair(1, next);
-    mfma_phase(F, cur, prev);
+    g1_phase(cur);
     if (set == 0) {
-      valu_phase();
+      ag2_phase(cur);
       pair_end();
       for (int i = 1; i < npair; ++i) {
         rotate();
         issue_pair(i + 1, next);
-        mfma_phase(T, cur, prev);
-        valu_phase();
+        g1_phase(cur);
+        ag2_phase(cur);
         pair_end();
       }
     } else {
@@ -1051,13 +1049,12 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       for (int i = 1; i < npair; ++i) {
         rotate();
         issue_pair(i + 1, next);
-        valu_phase();
-        mfma_phase(T, cur, prev);
+        ag2_phase(prev);
+        g1_phase(cur);
         pair_end();
       }
-      valu_phase();
+      ag2_phase(cur);
     }
-    g2_only(cur);
   } else {
     wait_vmcnt<0>();
   }

@@ -178,11 +178,14 @@ __device__ __forceinline__ u32x4 cat(const u32x2& lo, const u32x2& hi) {
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 constexpr unsigned BUF_OOB = 0x80000000u;  // an offset beyond every resource make_rsrc builds
 
-__device__ __forceinline__ Rsrc make_rsrc(const void* base, long long bytes) {
-  // the size is wave-uniform; readfirstlane keeps the resource in scalar registers
-  const int n = __builtin_amdgcn_readfirstlane(bytes <= 0 ? 0 : (bytes >= 0x7fffffffLL ? 0x7fffffff : (int)bytes));
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+// `bytes` must be wave-uniform and in [0, 2^31); readfirstlane keeps the resource in scalar
+// registers.
+__device__ __forceinline__ Rsrc make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, __builtin_amdgcn_readfirstlane(bytes),
+                                           0x00020000);
 }
+// min(max(v, 0), hi) with scalar-unit friendly selects (v, hi wave-uniform)
+__device__ __forceinline__ int clamp0(int v, int hi) { return v < 0 ? 0 : (v > hi ? hi : v); }
 __device__ __forceinline__ u32x4 buf_load16(Rsrc r, unsigned byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
 }
@@ -196,11 +199,10 @@ __device__ __forceinline__ u32x4 buf_load16(Rsrc r, unsigned byte_off) {
 // complete in issue order, so the compiler's own vmcnt waits stay correct (they can only
 // become stricter). The resource words are those of make_rsrc (stride 0, gfx9 format).
 typedef int i32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ i32x4 make_rsrc_words(const void* base, long long bytes) {
+__device__ __forceinline__ i32x4 make_rsrc_words(const void* base, int bytes) {
   const unsigned long long a = (unsigned long long)base;
-  const int n = bytes <= 0 ? 0 : (bytes >= 0x7fffffffLL ? 0x7fffffff : (int)bytes);
   i32x4 w = {__builtin_amdgcn_readfirstlane((int)(unsigned)a), __builtin_amdgcn_readfirstlane((int)((a >> 32) & 0xffffu)),
-             __builtin_amdgcn_readfirstlane(n), 0x00020000};
+             __builtin_amdgcn_readfirstlane(bytes), 0x00020000};
   return w;
 }
 __device__ __forceinline__ void buf_load16_lds(const i32x4& rsrc, unsigned byte_off, int lds_byte_off) {

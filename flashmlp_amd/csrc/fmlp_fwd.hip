@@ -66,8 +66,8 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   }
   auto load_chunk = [&](int c) {
     const int lim = E - c * 32;
-    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, (long long)D * E * 2 - 64LL * c);
-    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, (long long)min(max(lim, 0), 32) * D * 2);
+    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, D * E * 2 - 64 * c);
+    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
 #pragma unroll
     for (int k = 0; k < PPT / 2; ++k) {
       stg[k] = buf_load16(r1, (int)colq < lim ? offW1g[k] : BUF_OOB);
