@@ -6,10 +6,12 @@ A step is one flashmlp_fwd + flashmlp_bwd over the workload's synthetic inputs, 
 resident in HBM before the timed region. Prints ONE JSON line (rank 0 of one process).
 
 FLOP accounting: u = H*B*D*E; forward 4u, backward 8u, step 12u.
-`value` = 12u / wall-clock ms_per_step. `roofline` describes the dominant kernel (the
-unified backward, 8u per launch) with its duration from HIP events recorded on the
-stream the kernels run on. `cpu_baseline` times the CPU oracle (torch fp32 autograd of
-the restated reference path) on a bounded sample of the same workload.
+`value` = 12u / wall-clock ms_per_step. `roofline` describes the dominant launch, the
+backward entry point fmlp_bwd (its dW and dX kernels, 8u algorithmic FLOPs per call),
+with its duration from HIP events recorded on the stream the kernels run on; the
+per-kernel split is in the committed rocprofv3 summary. `cpu_baseline` times the CPU
+oracle (torch fp32 autograd of the restated reference path) on a bounded sample of the
+same workload.
 """
 from __future__ import annotations
 
@@ -57,16 +59,16 @@ def make_gpu_inputs(H, B, D, E, dtype, x_std, seed=0):
 
 
 def traffic_from_profile(workload):
-    """HBM bytes per backward launch from the committed rocprofv3 PMC summary
-    (FETCH_SIZE and WRITE_SIZE runs, each scaled by the same counter's reading for a
-    device copy of known size), or None when no summary exists for this workload."""
-    path = os.path.join(ROOT, "profiles", f"bwd_kernel_{workload}_traffic.txt")
+    """HBM bytes per backward call (dW + dX kernels) from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE runs, each scaled by the same counter's reading for
+    a device copy of known size), or None when no summary exists for this workload."""
+    path = os.path.join(ROOT, "profiles", f"bwd_{workload}_traffic.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         for line in f:
             key, _, val = line.partition("=")
-            if key.strip() == "hbm_bytes_per_launch_bwd":
+            if key.strip() == "hbm_bytes_per_call_bwd":
                 return int(float(val))
     return None
 
@@ -249,7 +251,7 @@ def main():
         "fwd_tflops": round(fwd_tf, 2),
         "bwd_tflops": round(bwd_tf, 2),
         "roofline": {
-            "kernel": "fmlp::bwd_kernel (unified dW/dX backward)",
+            "kernel": "fmlp_bwd call: fmlp::dw2_kernel + fmlp::dx2_kernel",
             "bound": "mfma",
             "achieved": round(bwd_tf, 2),
             "peak": peak,

@@ -1,18 +1,16 @@
 // FlashMLP backward kernels for gfx950 (MI355X).
 //
 // The reference's two program roles (flashmlp.py:360-373), launched as two kernels so each
-// gets its own register allocation (dW: one wave per SIMD, dX: two):
-//   * dW programs (dw_kernel, launched first): per head h, E-tile of 128 columns and a B-range. Four
-//     waves each own 32 of the E-tile's columns. X and dO rows of the B-range are streamed
-//     in 32-row subtiles through an LDS ring and used twice: row-wise as the A operand of
-//     the recomputed Z = X W1c and dH = dO W2c^T (W1c^T, W2c held in registers), and
-//     through ds_read_b64_tr_b16 as the B operand of dW2 += h^T dO and dW1^T += dZ^T X
-//     (flashmlp.py:247-329). h and dZ are cast to the io dtype before those contractions
-//     (flashmlp.py:297-320) and come straight from the MFMA C layout (lane = E column).
-//   * dX programs (dx_kernel): per head and B-tile; recompute Z^T and
-//     dH^T = W2c dO^T per 32-column E-chunk, dZ = dH * act'(Z) cast to the io dtype, and
-//     dX += dZ W1c^T (flashmlp.py:165-244). Same LDS ring and software pipeline as the
-//     forward kernel.
+// gets its own register allocation:
+//   * dW programs (dw2_kernel, launched first): per head, 128-column E-tile and B-range;
+//     recompute Z = X W1c and dH = dO W2c^T per 32-row subtile, then dW2 += h^T dO and
+//     dW1^T += dZ^T X (flashmlp.py:247-329). h and dZ are cast to the io dtype before those
+//     contractions (flashmlp.py:297-320) and come straight from the MFMA C layout
+//     (lane = E column).
+//   * dX programs (dx2_kernel, or dx_kernel for small problems): per head and B-tile;
+//     recompute Z^T and dH^T = W2c dO^T per 32-column E-chunk, dZ = dH * act'(Z) cast to the
+//     io dtype, and dX += dZ W1c^T (flashmlp.py:165-244).
+//   * dw_reduce_kernel sums the dW programs' fp32 partials when B is split.
 // Leaky ReLU uses the autograd slope at Z == 0 (0.01); the reference Triton kernel uses 1.
 #include "fmlp_device.h"
 #include "fmlp_launch.h"
@@ -20,14 +18,12 @@
 
 namespace fmlp {
 
-constexpr int BWD_NW = 4;            // waves per workgroup (both roles)
-constexpr int BWD_NT = BWD_NW * 64;  // threads
-constexpr int DW_ET = 128;           // E columns per dW program (32 per wave)
+constexpr int DW_ET = 128;           // E columns per dW program (32 per wave column group)
 constexpr int DW_BT = 32;            // rows per streamed subtile
-// dX workgroups: 4 waves (128 rows).
+// dX workgroups of the 4-wave form: 128 rows.
 __host__ __device__ constexpr int dx_waves(int D) { return D > 0 ? 4 : 4; }
 
-// dW epilogue shared by the dW kernels. C layout of the accumulators: lane = column d
+// dW epilogue. C layout of the accumulators: lane = column d
 // (32 nt + l32), rows e = e0 + 8 (i / 4) + 4 g + (i % 4). nS == 1 writes dW1, dW2 in the io
 // dtype; otherwise fp32 partials ws2[s][h][e][d] and ws1[s][h][e][d] (= dW1^T) for
 // dw_reduce_kernel.
@@ -70,256 +66,6 @@ __device__ __forceinline__ void dw_store(const f32x16 (&a1)[D / 32], const f32x1
       }
     }
   }
-}
-
-// ------------------------------------------------------------------------------------
-// dW role
-// ------------------------------------------------------------------------------------
-template <bool BF16, int D, int ACT>
-__device__ __forceinline__ void dw_role(const u16* __restrict__ X, const u16* __restrict__ W1,
-                                        const u16* __restrict__ W2, const u16* __restrict__ dO,
-                                        u16* __restrict__ dW1, u16* __restrict__ dW2, float* __restrict__ ws,
-                                        int H, int B, int E, int nE, int nS, int rows_per_split, int t) {
-  constexpr int KS = D / 16, NTN = D / 32;
-  constexpr unsigned SLOT = 128u * D;    // X subtile (64*D bytes) + dO subtile (64*D bytes)
-  constexpr unsigned DOOFF = 64u * D;
-  constexpr int NP = 8 * D;              // 16-byte pieces per subtile (half X, half dO)
-  constexpr int PPT = NP / BWD_NT;
-  static_assert(NP % (2 * BWD_NT) == 0, "pieces per thread");
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
-  // logical order (h, s, et) with et fastest: programs streaming the same rows are adjacent
-  const int et = t % nE;
-  const int hs = t / nE;
-  const int s = hs % nS, h = hs / nS;
-  const int e_prog = et * DW_ET;
-  const int e0 = e_prog + 32 * wave;
-  const int b_lo = s * rows_per_split;
-  const int b_hi = min(B, b_lo + rows_per_split);
-  const int nsub = (b_hi - b_lo + DW_BT - 1) / DW_BT;
-
-  const u16* Xh = X + (size_t)h * B * D;
-  const u16* dOh = dO + (size_t)h * B * D;
-  const u16* W1h = W1 + (size_t)h * D * E;
-  const u16* W2h = W2 + (size_t)h * E * D;
-
-  // ---- W1c^T (B operand of Z = X W1c) via LDS: W1[:, e_prog .. +128] as [D][128] rows ----
-  {
-    constexpr int NPW = D * (DW_ET / 8);
-#pragma unroll
-    for (int k = 0; k < NPW / BWD_NT; ++k) {
-      const int p = tid + k * BWD_NT;
-      const int d = p / (DW_ET / 8), q = p % (DW_ET / 8);
-      const int e = e_prog + q * 8;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (e < E) v = *(const u32x4*)(W1h + (size_t)d * E + e);
-      lds_write16((unsigned)(d * DW_ET * 2 + q * 16), v);
-    }
-  }
-  __syncthreads();
-  u32x4 w1t[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const unsigned col = 32 * wave + 16 * (G & 1) + 4 * (i16 & 3);
-    const unsigned r0 = 16 * ks + 8 * g + (i16 >> 2);
-    w1t[ks] = cat(lds_read_tr(r0 * (DW_ET * 2) + col * 2), lds_read_tr((r0 + 4) * (DW_ET * 2) + col * 2));
-  }
-  // W2c rows (B operand of dH = dO W2c^T): lane = column e, 8 consecutive d
-  u32x4 w2r[KS];
-#pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (e0 + l32 < E) v = *(const u32x4*)(W2h + (size_t)(e0 + l32) * D + ks * 16 + g * 8);
-    w2r[ks] = v;
-  }
-  __syncthreads();  // the W1 staging area becomes the subtile ring
-
-  // ---- subtile staging ----
-  // Branch-free buffer loads over the subtile's rows: rows past the B-range (and whole
-  // subtiles past the last one, loaded but never used) fall outside the resource.
-  u32x4 stg[PPT];
-  unsigned offSub[PPT / 2];
-#pragma unroll
-  for (int j = 0; j < PPT / 2; ++j) {
-    const unsigned p = tid + j * BWD_NT;
-    offSub[j] = (p / (D / 8)) * (D * 2u) + (p % (D / 8)) * 16u;  // row r, piece q
-  }
-  auto load_sub = [&](int k) {
-    const int r0 = b_lo + k * DW_BT;
-    const int bytes = clamp0(b_hi - r0, DW_BT) * D * 2;
-    const Rsrc rx = make_rsrc(Xh + (size_t)r0 * D, bytes);
-    const Rsrc rd = make_rsrc(dOh + (size_t)r0 * D, bytes);
-#pragma unroll
-    for (int j = 0; j < PPT / 2; ++j) {
-      stg[j] = buf_load16(rx, offSub[j]);
-      stg[PPT / 2 + j] = buf_load16(rd, offSub[j]);
-    }
-  };
-  auto store_sub = [&](int slot) {
-    const unsigned base = slot * SLOT;
-#pragma unroll
-    for (int j = 0; j < PPT; ++j) {
-      const int p = tid + (j % (PPT / 2)) * BWD_NT;
-      const int r = p / (D / 8), q = p % (D / 8);
-      lds_write16(base + (j < PPT / 2 ? 0u : DOOFF) + w2s_off(r, q), stg[j]);
-    }
-  };
-
-  // per-lane LDS offsets (slot relative). Subtiles are stored as D/32 blocks of
-  // [32 rows][32 columns] (w2s_off), so block, row-group and K-step displacements are
-  // immediates and only the lane part needs a register.
-  //   row-wise A operand: row l32, 16-byte piece 2ks + g  -> offRow[ks % 2] + (ks / 2) * 2048
-  unsigned offRow[2];
-#pragma unroll
-  for (int kp = 0; kp < 2; ++kp) offRow[kp] = w2s_off(l32, 2 * kp + g);
-  //   transposed B operand: rows 16s + 8r + 4g + i16/4, columns 32nt + 16(G%2) + 4(i16%4)
-  //   -> offTr[r] + nt * 2048 + s * 1024 (the chunk XOR depends on r and g only)
-  unsigned offTr[2];
-#pragma unroll
-  for (int r = 0; r < 2; ++r)
-    offTr[r] = w2s_off(8 * r + 4 * g + (i16 >> 2), 2 * (G & 1) + ((i16 & 3) >> 1)) + 8u * (i16 & 1);
-
-  f32x16 a2[NTN], a1[NTN];  // dW2 (e x d) and dW1^T (e x d) accumulators
-#pragma unroll
-  for (int nt = 0; nt < NTN; ++nt) {
-    a2[nt] = zero16();
-    a1[nt] = zero16();
-  }
-
-  auto gemm_zh = [&](int slot, f32x16& z, f32x16& dh) {
-    const unsigned base = slot * SLOT;
-    z = zero16();
-    dh = zero16();
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const u32x4 ax = lds_read16(base + offRow[ks & 1] + (ks >> 1) * 2048u);
-      const u32x4 ad = lds_read16(base + DOOFF + offRow[ks & 1] + (ks >> 1) * 2048u);
-      z = mfma<BF16>(ax, w1t[ks], z);
-      dh = mfma<BF16>(ad, w2r[ks], dh);
-    }
-  };
-  auto gemm_dw = [&](int slot, const u32x4 (&hT)[2], const u32x4 (&dzT)[2]) {
-    const unsigned base = slot * SLOT;
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) {
-        const unsigned o0 = offTr[0] + nt * 2048u + s2 * 1024u, o1 = offTr[1] + nt * 2048u + s2 * 1024u;
-        const u32x4 bdo = cat(lds_read_tr(base + DOOFF + o0), lds_read_tr(base + DOOFF + o1));
-        a2[nt] = mfma<BF16>(hT[s2], bdo, a2[nt]);
-        const u32x4 bx = cat(lds_read_tr(base + o0), lds_read_tr(base + o1));
-        a1[nt] = mfma<BF16>(dzT[s2], bx, a1[nt]);
-      }
-  };
-  auto activate = [&](const f32x16& z, const f32x16& dh, u32x4 (&hT)[2], u32x4 (&dzT)[2]) {
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        float h0, d0, h1, d1;
-        act_fb<ACT>(z[8 * s2 + 2 * w], dh[8 * s2 + 2 * w], h0, d0);
-        act_fb<ACT>(z[8 * s2 + 2 * w + 1], dh[8 * s2 + 2 * w + 1], h1, d1);
-        hT[s2][w] = pack2<BF16>(h0, h1);
-        dzT[s2][w] = pack2<BF16>(d0, d1);
-      }
-  };
-
-  if (nsub > 0) {
-    load_sub(0);
-    store_sub(0);
-    if (nsub > 1) {
-      load_sub(1);
-      store_sub(1);
-    }
-    load_sub(2);
-    __syncthreads();
-    // Pipeline state carried between iterations (ping-pong, no copies): Z and dH of the
-    // subtile to activate, and h, dZ of the previous subtile (A operands of the dW products).
-    struct St {
-      f32x16 z, dh;
-      u32x4 h[2], dz[2];
-    };
-    St sa, sb;
-    gemm_zh(0, sa.z, sa.dh);
-    // Iteration k reads `in` (Z, dH of subtile k; h, dZ of subtile k-1) and writes `out`
-    // (Z, dH of subtile k+1; h, dZ of subtile k): recompute Z, dH of subtile k+1 (group 1),
-    // accumulate dW over subtile k-1 (group 2) and activate subtile k, as a fixed sequence of
-    // steps: one MFMA each, operand reads PD steps ahead, activation spread over the steps.
-    auto iter = [&](auto G1, auto G2, int k, St& in, St& out) {
-      constexpr bool DO_G1 = decltype(G1)::value;
-      constexpr bool DO_G2 = decltype(G2)::value;
-      constexpr int N1 = DO_G1 ? 2 * KS : 0, N2 = DO_G2 ? 4 * NTN : 0, NOPS = N1 + N2;
-      constexpr int PD = 2;
-      const unsigned base1 = ((k + 1) & 3) * SLOT, base2 = ((k - 1) & 3) * SLOT;
-      store_sub((k + 2) & 3);                    // subtile k+2 (loaded during iteration k-1)
-      load_sub(k + 3);  // subtile k+3 -> registers
-      __builtin_amdgcn_sched_barrier(0);
-      auto fetch = [&](int j) -> u32x4 {
-        const int q = sched_index(j, N1, N2);
-        if (sched_is_g2(j, N1, N2)) {  // (s, nt, which): which 0 -> dW2 (B = dO^T), 1 -> dW1^T (B = X^T)
-          const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1, which = q & 1;
-          const unsigned bb = base2 + (which == 0 ? DOOFF : 0u) + nt * 2048u + s2 * 1024u;
-          return cat(lds_read_tr(bb + offTr[0]), lds_read_tr(bb + offTr[1]));
-        }
-        const int ks = q >> 1, which = q & 1;  // which 0 -> Z (A = X), 1 -> dH (A = dO)
-        return lds_read16(base1 + (which ? DOOFF : 0u) + offRow[ks & 1] + (ks >> 1) * 2048u);
-      };
-      float hv[16], dv[16];
-      u32x4 ring[PD + 1];
-#pragma unroll
-      for (int j = 0; j < PD && j < NOPS; ++j) ring[j] = fetch(j);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < NOPS; ++j) {
-        const u32x4 cur = ring[j % (PD + 1)];
-        if (j + PD < NOPS) ring[(j + PD) % (PD + 1)] = fetch(j + PD);
-        const int q = sched_index(j, N1, N2);
-        if (sched_is_g2(j, N1, N2)) {
-          const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1;
-          if ((q & 1) == 0) a2[nt] = mfma<BF16>(in.h[s2], cur, a2[nt]);
-          else a1[nt] = mfma<BF16>(in.dz[s2], cur, a1[nt]);
-        } else {
-          const int ks = q >> 1;  // ks == 0 starts the chain from a literal zero accumulator
-          if ((q & 1) == 0) out.z = mfma<BF16>(cur, w1t[ks], ks == 0 ? zero16() : out.z);
-          else out.dh = mfma<BF16>(cur, w2r[ks], ks == 0 ? zero16() : out.dh);
-        }
-#pragma unroll
-        for (int e = sched_elem_begin(j, NOPS, 16); e < sched_elem_begin(j + 1, NOPS, 16); ++e) {
-          act_fb<ACT>(in.z[e], in.dh[e], hv[e], dv[e]);
-          if (e & 1) {
-            out.h[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1], hv[e]);
-            out.dz[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
-          }
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      __syncthreads();
-    };
-    if (nsub == 1) {
-      activate(sa.z, sa.dh, sb.h, sb.dz);
-      gemm_dw(0, sb.h, sb.dz);
-    } else {
-      const std::true_type T{};
-      const std::false_type F{};
-      iter(T, F, 0, sa, sb);
-      int k = 1;
-      for (; k + 2 < nsub; k += 2) {
-        iter(T, T, k, sb, sa);
-        iter(T, T, k + 1, sa, sb);
-      }
-      if (k + 2 == nsub) {
-        iter(T, T, k, sb, sa);
-        iter(F, T, k + 1, sa, sb);
-        gemm_dw((nsub - 1) & 3, sb.h, sb.dz);
-      } else {
-        iter(F, T, k, sb, sa);
-        gemm_dw((nsub - 1) & 3, sa.h, sa.dz);
-      }
-    }
-  }
-
-  dw_store<BF16, D>(a1, a2, dW1, dW2, ws, H, E, h, s, nS, e0, g, l32);
 }
 
 // ------------------------------------------------------------------------------------
@@ -1094,17 +840,6 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   }
 }
 
-// dW programs: one wave per SIMD (the role keeps W1c^T / W2c fragments and both dW
-// accumulators in registers).
-template <bool BF16, int D, int ACT>
-__global__ void __launch_bounds__(BWD_NT)
-dw_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-          const u16* __restrict__ dO, u16* __restrict__ dW1, u16* __restrict__ dW2, float* __restrict__ ws,
-          int H, int B, int E, int nE, int nS, int rows_per_split) {
-  dw_role<BF16, D, ACT>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split,
-                        xcd_remap(blockIdx.x, gridDim.x));
-}
-
 // dX programs: 4 waves; at D = 64 two workgroups share a CU (two waves per SIMD), at
 // D = 128 the role needs more than 256 VGPRs and runs one wave per SIMD.
 template <bool BF16, int D, int ACT, int MT>
@@ -1157,7 +892,6 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus) {
   if (ns < 1) ns = 1;
   p.nS = (int)ns;
   p.rows_per_split = (int)rps;
-  p.dw_kind = env_int("FMLP_DW_KIND", 1) ? 1 : 0;
   // dX programs: 256 rows when that still gives >= 2 programs per CU, else 128
   // (D = 128 with two M-tiles per wave exceeds the register file, so it keeps one)
   // dX programs: the 8-wave form unless it would leave most CUs idle (measured on MI355X:
@@ -1179,23 +913,13 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   hipError_t e;
   // dW programs (and their partial reduction), then dX programs, in stream order
   if (p.n_dw > 0) {
-    if (p.dw_kind == 1) {
-      const size_t lds = 1280u * D;  // two weight tiles (256 D each) + three subtile pairs (256 D each)
-      auto k = dw2_kernel<BF16, D, ACT>;
-      e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                         (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws, (int)a.H,
-                         (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split);
-    } else {
-      const size_t lds = 4u * 128u * D > (size_t)D * DW_ET * 2 ? 4u * 128u * D : (size_t)D * DW_ET * 2;
-      auto k = dw_kernel<BF16, D, ACT>;
-      e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(BWD_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                         (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws, (int)a.H,
-                         (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split);
-    }
+    const size_t lds = 1280u * D;  // two weight tiles (256 D bytes each) + three subtile pairs (256 D each)
+    auto k = dw2_kernel<BF16, D, ACT>;
+    e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                       (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws, (int)a.H,
+                       (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (p.nS > 1) {

@@ -22,6 +22,7 @@ struct FwdArgs {
 // Backward work decomposition (chosen on the host, see plan_bwd):
 //   dW programs: H * nE * nS, each owning an E-tile of 128 columns and a B-range of
 //                rows_per_split rows (nS > 1 writes fp32 partials to the workspace).
+//                8 waves (two per SIMD), dw2_kernel.
 //   dX programs: H * dx_tiles_per_head, each owning dx_rows rows.
 struct BwdPlan {
   int nE;              // E-tiles of 128 per head
@@ -29,7 +30,6 @@ struct BwdPlan {
   int rows_per_split;  // multiple of 32
   int dx_mt;           // 32-row M-tiles per wave in dX programs (rows per program = 128 * dx_mt)
   int dx_kind;         // 0: 4-wave software-pipelined dX programs (128 rows); 1: 8-wave (256 rows)
-  int dw_kind;         // 0: 4-wave dW programs (one wave per SIMD); 1: 8-wave (two per SIMD)
   int dx_tiles_per_head;
   long long n_dw, n_dx;
   size_t ws_bytes;     // fp32 partials when nS > 1
