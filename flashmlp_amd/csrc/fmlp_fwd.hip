@@ -64,24 +64,43 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     offW1g[k] = (p >> 2) * (unsigned)E * 2u + (p & 3u) * 16u;                   // row d, piece q
     offW2g[k] = ((p >> 2) & 31u) * (D * 2u) + (p >> 7) * 64u + (p & 3u) * 16u;   // row er, block nt, piece q
   }
+  struct ChunkSrc {
+    Rsrc r1, r2;
+    int lim;
+  };
+  auto chunk_src = [&](int c) {
+    ChunkSrc cs;
+    cs.lim = E - c * 32;
+    cs.r1 = make_rsrc(W1h + (size_t)c * 32, D * E * 2 - 64 * c);
+    cs.r2 = make_rsrc(W2h + (size_t)c * 32 * D, clamp0(cs.lim, 32) * D * 2);
+    return cs;
+  };
+  auto load_piece = [&](const ChunkSrc& cs, int k) {
+    if (k < PPT / 2) stg[k] = buf_load16(cs.r1, (int)colq < cs.lim ? offW1g[k] : BUF_OOB);
+    else stg[k] = buf_load16(cs.r2, offW2g[k - PPT / 2]);
+  };
+  auto store_piece = [&](int slot, int k) {
+    const unsigned base = slot * SLOT;
+    const unsigned p = tid + (k % (PPT / 2)) * NT;
+    if (k < PPT / 2) lds_write16(base + p * 16u, stg[k]);  // d*64 + q*16
+    else lds_write16(base + W2OFF + (p >> 7) * 2048u + ((p >> 2) & 31u) * 64u + (p & 3u) * 16u, stg[k]);
+  };
   auto load_chunk = [&](int c) {
-    const int lim = E - c * 32;
-    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, D * E * 2 - 64 * c);
-    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
+    const ChunkSrc cs = chunk_src(c);
 #pragma unroll
-    for (int k = 0; k < PPT / 2; ++k) {
-      stg[k] = buf_load16(r1, (int)colq < lim ? offW1g[k] : BUF_OOB);
-      stg[PPT / 2 + k] = buf_load16(r2, offW2g[k]);
-    }
+    for (int k = 0; k < PPT; ++k) load_piece(cs, k);
   };
   auto store_chunk = [&](int slot) {
-    const unsigned base = slot * SLOT;
 #pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      const unsigned p = tid + (k % (PPT / 2)) * NT;
-      if (k < PPT / 2) lds_write16(base + p * 16u, stg[k]);  // d*64 + q*16
-      else lds_write16(base + W2OFF + (p >> 7) * 2048u + ((p >> 2) & 31u) * 64u + (p & 3u) * 16u, stg[k]);
-    }
+    for (int k = 0; k < PPT; ++k) store_piece(slot, k);
+  };
+  // end of a chunk: the LDS stores are retired and visible after the barrier; the loads of
+  // the chunk after next stay in flight (their data is waited for where it is stored)
+  auto chunk_end = [&]() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   };
 
   // ---- X rows -> registers (B operand of Z^T = W1c^T X^T: lane = row b, 8 consecutive d) ----
@@ -122,7 +141,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     store_chunk(1);
   }
   load_chunk(2);
-  __syncthreads();
+  chunk_end();
   // Pipeline state carried between iterations: Z^T of the chunk to activate and h of the
   // previous chunk (A operand of O += h W2c, two K steps). Iterations run in pairs with the
   // two state copies swapping roles, so nothing is copied between iterations.
@@ -146,9 +165,12 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     constexpr int PER = 16 / NOPS;  // activation elements per step
     const unsigned base1 = ((c + 1) & 3) * SLOT, base2 = ((c - 1) & 3) * SLOT;
 
-    store_chunk((c + 2) & 3);  // chunk c+2 (loaded during iteration c-1)
-    load_chunk(c + 3);         // chunk c+3 -> registers
-    __builtin_amdgcn_sched_barrier(0);
+    // chunk c+2 (loaded during iteration c-1) goes to its slot and chunk c+3 is loaded into
+    // the same registers, one 16-byte piece per step (store of piece k at step 2k, its next
+    // load at step 2k+1)
+    const int sslot = (c + 2) & 3;
+    const ChunkSrc cs = chunk_src(c + 3);
+    static_assert(2 * PPT <= KS, "staging steps");
 
     // op j: G1 and G2 alternate when both are present
     auto is_g1 = [&](int j) { return DO_G1 && (!DO_G2 || (j % 2 == 0)); };
@@ -166,6 +188,10 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       if (j + 2 < NOPS) {
         const u32x4 nx = fetch(j + 2);
         if ((j + 2) % 3 == 0) op0 = nx; else if ((j + 2) % 3 == 1) op1 = nx; else op2 = nx;
+      }
+      if (j < 2 * PPT) {
+        if ((j & 1) == 0) store_piece(sslot, j >> 1);
+        else load_piece(cs, j >> 1);
       }
       const int k = idx(j);
       if (is_g1(j)) {  // k == 0 starts the chain from a literal zero accumulator
@@ -186,7 +212,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();
+    chunk_end();
   };
   auto last_gemm2 = [&](const St& st) {
     const unsigned base2 = ((NC - 1) & 3) * SLOT;
