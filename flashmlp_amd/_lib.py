@@ -14,6 +14,8 @@ LIB_PATH = Path(__file__).resolve().with_name("libflashmlp.so")
 FMLP_OK = 0
 FMLP_DTYPE_F16 = 0
 FMLP_DTYPE_BF16 = 1
+# OR-ed into the dtype code: outputs are fp32 arrays holding the unrounded fp32 sums
+FMLP_OUT_F32 = 0x100
 ACT_CODES = {"": 0, "silu": 1, "leaky_relu": 2, "sigmoid": 3}
 
 # (name, restype, argtypes) for every symbol include/flashmlp.h declares

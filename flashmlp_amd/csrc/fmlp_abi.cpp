@@ -65,8 +65,10 @@ int check_shape(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   if (H < 0 || B < 0 || D < 0 || E < 0)
     return fail(FMLP_ERR_INVALID_ARG, "negative dimension (H=%lld B=%lld D=%lld E=%lld)", (long long)H,
                 (long long)B, (long long)D, (long long)E);
-  if (dtype != FMLP_DTYPE_F16 && dtype != FMLP_DTYPE_BF16)
-    return fail(FMLP_ERR_UNSUPPORTED, "dtype code %d: only fp16 (0) and bf16 (1) are supported", dtype);
+  const int io = dtype & ~FMLP_OUT_F32;
+  if (io != FMLP_DTYPE_F16 && io != FMLP_DTYPE_BF16)
+    return fail(FMLP_ERR_UNSUPPORTED, "dtype code %d: only fp16 (0) and bf16 (1) are supported, optionally with FMLP_OUT_F32",
+                dtype);
   if (D != 64 && D != 128) return fail(FMLP_ERR_UNSUPPORTED, "hidden dimension D=%lld: supported D are 64 and 128", (long long)D);
   if (E < 8 || E % 8 != 0)
     return fail(FMLP_ERR_UNSUPPORTED, "intermediate dimension E=%lld: must be a positive multiple of 8", (long long)E);
@@ -137,7 +139,7 @@ FMLP_EXPORT int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o,
       (st = check_ptr(o, "o", rows)))
     return st;
   if (!rows) return ok();
-  fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, dtype == FMLP_DTYPE_BF16, act};
+  fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, (dtype & ~FMLP_OUT_F32) == FMLP_DTYPE_BF16, act, (dtype & FMLP_OUT_F32) != 0};
   hipError_t e = fmlp::launch_fwd(a, (hipStream_t)stream);
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
   return ok();
@@ -171,7 +173,8 @@ FMLP_EXPORT int fmlp_bwd(const void* x, const void* w1, const void* w2, const vo
       return fail(FMLP_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, plan.ws_bytes);
     if (!aligned16(workspace)) return fail(FMLP_ERR_INVALID_ARG, "workspace is not 16-byte aligned");
   }
-  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, dtype == FMLP_DTYPE_BF16, act, workspace};
+  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, (dtype & ~FMLP_OUT_F32) == FMLP_DTYPE_BF16, act, workspace,
+                  (dtype & FMLP_OUT_F32) != 0};
   hipError_t e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return ok();

@@ -25,16 +25,34 @@ __host__ __device__ constexpr int dx_waves(int D) { return D > 0 ? 4 : 4; }
 
 // dW epilogue. C layout of the accumulators: lane = column d
 // (32 nt + l32), rows e = e0 + 8 (i / 4) + 4 g + (i % 4). nS == 1 writes dW1, dW2 in the io
-// dtype; otherwise fp32 partials ws2[s][h][e][d] and ws1[s][h][e][d] (= dW1^T) for
-// dw_reduce_kernel.
+// dtype (fp32 when outf32); otherwise fp32 partials ws2[s][h][e][d] and ws1[s][h][e][d]
+// (= dW1^T) for dw_reduce_kernel.
 template <bool BF16, int D>
-__device__ __forceinline__ void dw_store(const f32x16 (&a1)[D / 32], const f32x16 (&a2)[D / 32], u16* __restrict__ dW1,
-                                         u16* __restrict__ dW2, float* __restrict__ ws, int H, int E, int h, int s,
-                                         int nS, int e0, int g, int l32) {
+__device__ __forceinline__ void dw_store(const f32x16 (&a1)[D / 32], const f32x16 (&a2)[D / 32], void* __restrict__ dW1,
+                                         void* __restrict__ dW2, float* __restrict__ ws, int H, int E, int h, int s,
+                                         int nS, int e0, int g, int l32, int outf32) {
   constexpr int NTN = D / 32;
-  if (nS == 1) {
-    u16* dW2h = dW2 + (size_t)h * E * D;
-    u16* dW1h = dW1 + (size_t)h * D * E;
+  if (nS == 1 && outf32) {
+    float* dW2h = (float*)dW2 + (size_t)h * E * D;
+    float* dW1h = (float*)dW1 + (size_t)h * D * E;
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int eb = e0 + 8 * i4 + 4 * g;
+      if (eb < E) {
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) {
+          const int d = nt * 32 + l32;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            dW2h[(size_t)(eb + j) * D + d] = a2[nt][4 * i4 + j];
+            dW1h[(size_t)d * E + eb + j] = a1[nt][4 * i4 + j];
+          }
+        }
+      }
+    }
+  } else if (nS == 1) {
+    u16* dW2h = (u16*)dW2 + (size_t)h * E * D;
+    u16* dW1h = (u16*)dW1 + (size_t)h * D * E;
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int eb = e0 + 8 * i4 + 4 * g;  // 4 consecutive columns eb .. eb+3 (E % 8 == 0)
@@ -68,13 +86,42 @@ __device__ __forceinline__ void dw_store(const f32x16 (&a1)[D / 32], const f32x1
   }
 }
 
+// Store of a wave's 32-row dX tile (C layout: lane = column d = 32 nt + l32, rows
+// b0 + 8 (i / 4) + 4 g + (i % 4)); rows at or past B are not written.
+template <bool BF16, int D>
+__device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], void* __restrict__ out, size_t head_off, int B,
+                                           int b0, int g, int l32, int outf32) {
+  constexpr int NTN = D / 32;
+  if (outf32) {
+    float* o = (float*)out + head_off;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int b = b0 + 8 * (i >> 2) + 4 * g + (i & 3);
+      if (b < B) {
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) o[(size_t)b * D + nt * 32 + l32] = acc[nt][i];
+      }
+    }
+  } else {
+    u16* o = (u16*)out + head_off;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int b = b0 + 8 * (i >> 2) + 4 * g + (i & 3);
+      if (b < B) {
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) o[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(acc[nt][i]);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------
 // dX role
 // ------------------------------------------------------------------------------------
 template <bool BF16, int D, int ACT, int MT, int DXW>
 __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __restrict__ W1,
                                         const u16* __restrict__ W2, const u16* __restrict__ dO,
-                                        u16* __restrict__ dX, int B, int E, int tiles_per_head, int t) {
+                                        void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32, int t) {
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr int BB = DXW * MT * 32;
   constexpr unsigned SLOT = 128u * D;
@@ -92,7 +139,6 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
   const u16* dOh = dO + (size_t)h * B * D;
   const u16* W1h = W1 + (size_t)h * D * E;
   const u16* W2h = W2 + (size_t)h * E * D;
-  u16* dXh = dX + (size_t)h * B * D;
   const int b_wave = bt * BB + wave * MT * 32;
 
   // Branch-free buffer loads (as in the forward kernel): W2c rows past E fall outside the
@@ -314,15 +360,7 @@ __device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __
   }
 
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int b = b_wave + mt * 32 + 8 * (i >> 2) + 4 * g + (i & 3);
-      if (b < B) {
-#pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) dXh[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(acc[mt][nt][i]);
-      }
-    }
+  for (int mt = 0; mt < MT; ++mt) store_rows<BF16, D>(acc[mt], dX, (size_t)h * B * D, B, b_wave + mt * 32, g, l32, outf32);
 }
 
 // ------------------------------------------------------------------------------------
@@ -359,7 +397,7 @@ constexpr int DX2_ROWS = DX2_NW * 32;
 template <bool BF16, int D, int ACT>
 __global__ void __launch_bounds__(DX2_NT)
 dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-           const u16* __restrict__ dO, u16* __restrict__ dX, int B, int E, int tiles_per_head) {
+           const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr unsigned SLOT = 128u * D;
   constexpr unsigned W2OFF = 64u * D;
@@ -379,7 +417,6 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const u16* dOh = dO + (size_t)h * B * D;
   const u16* W1h = W1 + (size_t)h * D * E;
   const u16* W2h = W2 + (size_t)h * E * D;
-  u16* dXh = dX + (size_t)h * B * D;
   const int b_wave = bt * DX2_ROWS + wave * 32;
 
   // ---- staging pieces: piece p (16 bytes at slot offset 16 p) of a chunk ----
@@ -556,15 +593,7 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     valu_phase();
   }
   g2_only(NC - 1);
-
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int b = b_wave + 8 * (i >> 2) + 4 * g + (i & 3);
-    if (b < B) {
-#pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) dXh[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(acc[nt][i]);
-    }
-  }
+  store_rows<BF16, D>(acc, dX, (size_t)h * B * D, B, b_wave, g, l32, outf32);
 }
 
 // ------------------------------------------------------------------------------------
@@ -593,8 +622,8 @@ __device__ __forceinline__ unsigned wt_off(unsigned r, unsigned q) {
 template <bool BF16, int D, int ACT>
 __global__ void __launch_bounds__(DW2_NT)
 dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-           const u16* __restrict__ dO, u16* __restrict__ dW1, u16* __restrict__ dW2, float* __restrict__ ws,
-           int H, int B, int E, int nE, int nS, int rows_per_split) {
+           const u16* __restrict__ dO, void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
+           int H, int B, int E, int nE, int nS, int rows_per_split, int outf32) {
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr int SUB = 64 * D;            // bytes of a [32][D] subtile
   constexpr int PAIR = 4 * SUB;          // X set0, dO set0, X set1, dO set1
@@ -835,7 +864,7 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
             a1[nt][4 * i4 + j] += __uint_as_float(v1[j]);
           }
         }
-      dw_store<BF16, D>(a1, a2, dW1, dW2, ws, H, E, h, s, nS, e0, g, l32);
+      dw_store<BF16, D>(a1, a2, dW1, dW2, ws, H, E, h, s, nS, e0, g, l32, outf32);
     }
   }
 }
@@ -845,23 +874,24 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 template <bool BF16, int D, int ACT, int MT>
 __global__ void __launch_bounds__(dx_waves(D) * 64)
 dx_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-          const u16* __restrict__ dO, u16* __restrict__ dX, int B, int E, int tiles_per_head) {
-  dx_role<BF16, D, ACT, MT, dx_waves(D)>(X, W1, W2, dO, dX, B, E, tiles_per_head,
+          const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
+  dx_role<BF16, D, ACT, MT, dx_waves(D)>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32,
                                          xcd_remap(blockIdx.x, gridDim.x));
 }
 
 // Sum of the nS fp32 partials; dW2 keeps the (e, d) layout, dW1 is written transposed.
 template <bool BF16>
 __global__ void __launch_bounds__(256)
-dw_reduce_kernel(const float* __restrict__ ws, u16* __restrict__ dW1, u16* __restrict__ dW2, int H, int E, int D,
-                 int nS) {
+dw_reduce_kernel(const float* __restrict__ ws, void* __restrict__ dW1, void* __restrict__ dW2, int H, int E, int D,
+                 int nS, int outf32) {
   const size_t per = (size_t)H * E * D;
   const size_t stride = (size_t)gridDim.x * blockDim.x;
   for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < per; idx += stride) {
     // dW2[h][e][d]
     float s2 = 0.f;
     for (int s = 0; s < nS; ++s) s2 += ws[(size_t)s * per + idx];
-    dW2[idx] = from_f32<BF16>(s2);
+    if (outf32) ((float*)dW2)[idx] = s2;
+    else ((u16*)dW2)[idx] = from_f32<BF16>(s2);
     // dW1[h][d][e] from ws1[s][h][e][d]
     const size_t h = idx / ((size_t)D * E);
     const size_t rem = idx - h * (size_t)D * E;
@@ -869,7 +899,8 @@ dw_reduce_kernel(const float* __restrict__ ws, u16* __restrict__ dW1, u16* __res
     const size_t src = (h * E + e) * D + d;
     float s1 = 0.f;
     for (int s = 0; s < nS; ++s) s1 += ws[(size_t)(nS + s) * per + src];
-    dW1[idx] = from_f32<BF16>(s1);
+    if (outf32) ((float*)dW1)[idx] = s1;
+    else ((u16*)dW1)[idx] = from_f32<BF16>(s1);
   }
 }
 
@@ -918,8 +949,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                       (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dw1, (u16*)a.dw2, (float*)a.ws, (int)a.H,
-                       (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split);
+                       (const u16*)a.w2, (const u16*)a.dout, a.dw1, a.dw2, (float*)a.ws, (int)a.H,
+                       (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, a.out_f32 ? 1 : 0);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (p.nS > 1) {
@@ -927,7 +958,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
       size_t blocks = (per + 255) / 256;
       if (blocks > 8192) blocks = 8192;
       hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws,
-                         (u16*)a.dw1, (u16*)a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS);
+                         a.dw1, a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
@@ -938,7 +969,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
       hipError_t r = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (r != hipSuccess) return r;
       hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(dx_waves(D) * 64), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                         (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head);
+                         (const u16*)a.w2, (const u16*)a.dout, a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head,
+                         a.out_f32 ? 1 : 0);
       return hipGetLastError();
     };
     if (p.dx_kind == 1) {
@@ -947,7 +979,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
       e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(DX2_NT), lds2, st, (const u16*)a.x, (const u16*)a.w1,
-                         (const u16*)a.w2, (const u16*)a.dout, (u16*)a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head);
+                         (const u16*)a.w2, (const u16*)a.dout, a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head,
+                         a.out_f32 ? 1 : 0);
       e = hipGetLastError();
     } else {
       e = launch(dx_kernel<BF16, D, ACT, 1>);

@@ -29,7 +29,7 @@ namespace fmlp {
 template <bool BF16, int D, int ACT>
 __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-           u16* __restrict__ O, int B, int E, int tiles_per_head) {
+           void* __restrict__ O, int B, int E, int tiles_per_head, int outf32) {
   constexpr int NW = 4, NT = NW * 64;  // waves, threads
   constexpr int KS = D / 16;           // K steps of GEMM1 (= GEMM2 operand count 2 * D/32)
   constexpr int NTN = D / 32;          // N tiles of GEMM2
@@ -48,7 +48,6 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const u16* Xh = X + (size_t)h * B * D;
   const u16* W1h = W1 + (size_t)h * D * E;
   const u16* W2h = W2 + (size_t)h * E * D;
-  u16* Oh = O + (size_t)h * B * D;
   const int b_wave = bt * BB + wave * 32;
 
   // ---- chunk staging: global -> registers (one chunk ahead) -> LDS ----
@@ -247,13 +246,27 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     }
   }
 
-  // ---- epilogue: O tile (C layout: lane = column d, rows 8(i/4) + 4g + i%4) ----
+  // ---- epilogue: O tile (C layout: lane = column d, rows 8(i/4) + 4g + i%4); fp32 sums
+  // when the caller asked for them (FMLP_OUT_F32), else rounded to the io dtype ----
+  if (outf32) {
+    float* Oh = (float*)O + (size_t)h * B * D;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int b = b_wave + 8 * (i >> 2) + 4 * g + (i & 3);
-    if (b < B) {
+    for (int i = 0; i < 16; ++i) {
+      const int b = b_wave + 8 * (i >> 2) + 4 * g + (i & 3);
+      if (b < B) {
 #pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) Oh[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(o[nt][i]);
+        for (int nt = 0; nt < NTN; ++nt) Oh[(size_t)b * D + nt * 32 + l32] = o[nt][i];
+      }
+    }
+  } else {
+    u16* Oh = (u16*)O + (size_t)h * B * D;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int b = b_wave + 8 * (i >> 2) + 4 * g + (i & 3);
+      if (b < B) {
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) Oh[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(o[nt][i]);
+      }
     }
   }
 }
@@ -273,7 +286,7 @@ static hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(256), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                     (const u16*)a.w2, (u16*)a.o, (int)a.B, (int)a.E, tiles_per_head);
+                     (const u16*)a.w2, a.o, (int)a.B, (int)a.E, tiles_per_head, a.out_f32 ? 1 : 0);
   return hipGetLastError();
 }
 

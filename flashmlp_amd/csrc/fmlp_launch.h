@@ -17,6 +17,7 @@ struct FwdArgs {
   int64_t H, B, D, E;
   bool bf16;
   int act;
+  bool out_f32;  // outputs as fp32 (FMLP_OUT_F32)
 };
 
 // Backward work decomposition (chosen on the host, see plan_bwd):
@@ -47,6 +48,7 @@ struct BwdArgs {
   bool bf16;
   int act;
   void* ws;
+  bool out_f32;  // outputs as fp32 (FMLP_OUT_F32)
 };
 
 BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus);

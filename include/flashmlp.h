@@ -38,6 +38,13 @@ typedef enum {
 
 typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1 } fmlp_dtype;
 
+/* OR-ed into the dtype argument of fmlp_fwd / fmlp_bwd: the outputs (o; dx, dw1, dw2) are
+ * written as fp32 arrays of the same shapes, holding the fp32-accumulated sums before their
+ * final rounding to the io dtype. Inputs stay in the io dtype. A test and diagnostic
+ * variant with no counterpart in the reference: it lets callers check the accumulations
+ * against an fp32 emulation of the reference's algorithm at 1e-4 relative. */
+#define FMLP_OUT_F32 0x100
+
 /* Activation codes; names as in the reference ("", "silu", "leaky_relu", "sigmoid"). */
 typedef enum { FMLP_ACT_NONE = 0, FMLP_ACT_SILU = 1, FMLP_ACT_LEAKY_RELU = 2, FMLP_ACT_SIGMOID = 3 } fmlp_act;
 

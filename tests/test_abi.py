@@ -68,6 +68,11 @@ def test_shape_support(L):
     assert L.fmlp_shape_supported(2, 8, 96, 64, 1) == 0   # D
     assert L.fmlp_shape_supported(2, 8, 64, 12, 1) == 0   # E % 8
     assert L.fmlp_shape_supported(2, 8, 64, 64, 2) == 0   # dtype
+    # the fp32-output flag is accepted on either io dtype and nothing else
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_OUT_F32) == 1
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 0 | _lib.FMLP_OUT_F32) == 1
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 2 | _lib.FMLP_OUT_F32) == 0
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | 0x200) == 0
     assert L.fmlp_shape_supported(-1, 8, 64, 64, 1) == 0
 
 

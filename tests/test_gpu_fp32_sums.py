@@ -1,0 +1,110 @@
+"""fp32-accumulated sums of the gfx950 kernels against the cast-point oracle at 1e-4 relative.
+
+BASELINE.json's north star asks for 1e-4 relative on the fp32-accumulated sums. The io
+outputs (O, dX, dW1, dW2) are those sums rounded to bf16/fp16, whose own rounding step
+(2^-9 / 2^-12 relative) hides anything finer; the C ABI's FMLP_OUT_F32 flag has every output
+written as the fp32 sum before that rounding, so the sums can be compared directly with the
+oracle's (oracle.emulate with round_out=False: fp32 products of the io-quantised inputs with
+h and dZ rounded at the reference's cast points, flashmlp.py:141-157, 227-235, 297-321).
+
+Bar: normwise relative error <= 1e-4 per output tensor. What remains besides summation
+order is the rare one-ulp flip of an io-rounded intermediate (h or dZ) whose fp32 value sits
+on a rounding boundary; its share is printed.
+
+The cases cover both dX kernels (4-wave for small problems, 8-wave for large) and both dW
+store paths (direct when one B split suffices, fp32 partials + reduction otherwise).
+"""
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from flashmlp_amd import _lib
+from oracle import emulate
+from oracle.inputs import CONFIGS, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+BAR = 1e-4
+_DT = {torch.float16: _lib.FMLP_DTYPE_F16, torch.bfloat16: _lib.FMLP_DTYPE_BF16}
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _normrel(a, b):
+    a = a.double()
+    b = b.double()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def fp32_sums(x, w1, w2, do, act):
+    """Runs fmlp_fwd and fmlp_bwd with FMLP_OUT_F32 on the current device and stream."""
+    L = _lib.lib()
+    H, B, D = x.shape
+    E = w1.shape[2]
+    code = _DT[x.dtype] | _lib.FMLP_OUT_F32
+    a = _lib.ACT_CODES[act]
+    dev = x.device
+    stream = ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+    o = torch.empty(H, B, D, dtype=torch.float32, device=dev)
+    dx = torch.empty(H, B, D, dtype=torch.float32, device=dev)
+    dw1 = torch.empty(H, D, E, dtype=torch.float32, device=dev)
+    dw2 = torch.empty(H, E, D, dtype=torch.float32, device=dev)
+    _lib.check(L.fmlp_fwd(_ptr(x), _ptr(w1), _ptr(w2), _ptr(o), H, B, D, E, code, a, stream), "fp32-sum forward")
+    n = L.fmlp_bwd_workspace_bytes(H, B, D, E, code)
+    ws = torch.empty(max(n, 16), dtype=torch.uint8, device=dev)
+    _lib.check(L.fmlp_bwd(_ptr(x), _ptr(w1), _ptr(w2), _ptr(do), _ptr(dx), _ptr(dw1), _ptr(dw2), H, B, D, E, code, a,
+                          _ptr(ws), n, stream), "fp32-sum backward")
+    torch.cuda.synchronize()
+    return o, dx, dw1, dw2
+
+
+def run_sums(name, H, B, D, E, dtype, act, x_std=1.0, seed=0, heads=None):
+    x, w1, w2, do = make_inputs(H, B, D, E, dtype, x_std, seed)
+    _say(f"[fp32-sums] {name}: H={H} B={B} D={D} E={E} {dtype} act='{act}' seed={seed}")
+    o, dx, dw1, dw2 = fp32_sums(*(t.cuda() for t in (x, w1, w2, do)), act)
+    hs = list(range(H)) if heads is None else heads
+    xs, w1s, w2s, dos = (t[hs] for t in (x, w1, w2, do))
+    eo = emulate.emu_fwd(xs, w1s, w2s, act, dtype, round_out=False)
+    edx, edw1, edw2 = emulate.emu_bwd(xs, w1s, w2s, dos, act, dtype, round_out=False)
+    res = {}
+    for k, g, e in (("o", o, eo), ("dx", dx, edx), ("dw1", dw1, edw1), ("dw2", dw2, edw2)):
+        g = g[hs].cpu()
+        assert torch.isfinite(g).all(), k
+        res[k] = _normrel(g, e)
+    _say(f"[fp32-sums] {name}: " + " ".join(f"{k}_rel={v:.3g}" for k, v in res.items()))
+    assert max(res.values()) <= BAR, res
+    return res
+
+
+SMALL = [(dt, D, act) for dt in (torch.float16, torch.bfloat16) for D in (64, 128)
+         for act in ("", "silu", "leaky_relu", "sigmoid")]
+
+
+@pytest.mark.parametrize("dt,D,act", SMALL, ids=[f"{str(d).split('.')[-1]}-D{D}-{a or 'linear'}" for d, D, a in SMALL])
+def test_small_sums(dt, D, act):
+    run_sums("small", 3, 200, D, 96, dt, act, seed=1)
+
+
+def test_tail_sums():
+    run_sums("tail", 2, 129, 128, 264, torch.bfloat16, "silu", seed=2)
+    run_sums("tail", 2, 33, 64, 40, torch.float16, "sigmoid", seed=3)
+
+
+def test_split_reduction_sums():
+    # 12 x 1024 x 64 x 768: the dW programs split B and reduce fp32 partials
+    run_sums("ref-test-shape", 12, 1024, 64, 768, torch.bfloat16, "silu", seed=42)
+
+
+@pytest.mark.parametrize("name", ["cfg3", "cfg4"])
+def test_config_sums(name):
+    c = CONFIGS[name]
+    run_sums(name, c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=[0, c.H - 1])
