@@ -5,17 +5,19 @@
 // point, flashmlp.py:137-150) and O to the io dtype at the store (flashmlp.py:157).
 // The (H, B, E) intermediate never leaves registers.
 //
-// Per workgroup: NW waves, each owning MT 32-row M-tiles (BB = 32*MT*NW rows).
+// Per workgroup: D/16 waves (two per SIMD), each owning one 32-row M-tile (256 rows per
+// workgroup at D = 128, 128 at D = 64).
 //   * X rows live in registers for the whole kernel, already in the MFMA B-operand layout
 //     of Z^T = W1c^T X^T (lane = row b, 8 consecutive d).
 //   * E is walked in 32-column chunks. Chunk k's W1c (D x 32) and W2c (32 x D) tiles are
-//     staged in an LDS ring of 4 slots; both are read with ds_read_b64_tr_b16, which
+//     staged in an LDS ring of 8 slots; both are read with ds_read_b64_tr_b16, which
 //     yields the K-contiguous operands straight from the natural row-major tiles.
 //   * Z^T is produced in the MFMA C layout (lane = column b), which is exactly the A
 //     operand layout of O += h W2c (lane = row b), so h never round-trips through LDS.
 //   * Software pipeline, iteration c:  Z^T(c+1) = W1c(c+1)^T X^T  and  O += h(c-1) W2c(c-1)
-//     on the matrix cores while h(c) = act(Z^T(c)) runs on the VALU. The chunk c+2 is
-//     prefetched into registers and written to the free slot; one barrier per chunk.
+//     on the matrix cores while h(c) = act(Z^T(c)) runs on the VALU. Chunk c+4 is loaded
+//     straight into its LDS slot (buffer loads with the LDS destination, no registers and
+//     no LDS store instructions); one barrier per chunk.
 #include "fmlp_device.h"
 #include "fmlp_launch.h"
 #include <type_traits>
@@ -26,18 +28,24 @@ namespace fmlp {
 // 32-lane phase, which covers all 64 banks once):
 //   W1c  [D][32]           row d = W1[h][d][32c .. 32c+31]
 //   W2c  [D/32][32][32]    block nt, row e = W2[h][32c + e][32nt .. 32nt+31]
+// Waves per workgroup: one 32-row M-tile each, so that the workgroup's threads cover a chunk's
+// 4 D pieces of W1c and of W2c exactly once (NT == 4 D); two waves per SIMD either way.
+__host__ __device__ constexpr int fwd_waves(int D) { return D / 16; }
+constexpr int FWD_NSLOT = 8;  // LDS ring slots (chunks)
+constexpr int FWD_PF = 4;     // chunks loaded ahead
+
 template <bool BF16, int D, int ACT>
-__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(fwd_waves(D) * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            void* __restrict__ O, int B, int E, int tiles_per_head, int outf32) {
-  constexpr int NW = 4, NT = NW * 64;  // waves, threads
+  constexpr int NW = fwd_waves(D), NT = NW * 64;  // waves, threads
   constexpr int KS = D / 16;           // K steps of GEMM1 (= GEMM2 operand count 2 * D/32)
   constexpr int NTN = D / 32;          // N tiles of GEMM2
   constexpr int BB = NW * 32;          // rows per workgroup (32 per wave)
   constexpr unsigned SLOT = 128u * D;  // bytes per ring slot: W1c (64*D) + W2c (64*D)
   constexpr unsigned W2OFF = 64u * D;
-  constexpr int PPT = 8 * D / NT;      // 16-byte pieces per thread per chunk (half W1c, half W2c)
-  static_assert(PPT % 2 == 0, "pieces per thread");
+  constexpr int NSLOT = FWD_NSLOT, PF = FWD_PF;
+  static_assert(PF >= 2 && PF <= NSLOT - 2 && (NSLOT & (NSLOT - 1)) == 0, "ring");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
@@ -54,48 +62,28 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   // Branch-free buffer loads: W2c rows past E fall outside the chunk's resource; W1c
   // columns past E (last chunk when E % 32 != 0) get an out-of-range offset. Chunks past
   // the last one are loaded but never used.
-  u32x4 stg[PPT];
-  const unsigned colq = (tid & 3) * 8;  // first column of this thread's W1c pieces
-  unsigned offW1g[PPT / 2], offW2g[PPT / 2];
-#pragma unroll
-  for (int k = 0; k < PPT / 2; ++k) {
-    const unsigned p = tid + k * NT;
-    offW1g[k] = (p >> 2) * (unsigned)E * 2u + (p & 3u) * 16u;                   // row d, piece q
-    offW2g[k] = ((p >> 2) & 31u) * (D * 2u) + (p >> 7) * 64u + (p & 3u) * 16u;   // row er, block nt, piece q
-  }
-  struct ChunkSrc {
-    Rsrc r1, r2;
-    int lim;
-  };
-  auto chunk_src = [&](int c) {
-    ChunkSrc cs;
-    cs.lim = E - c * 32;
-    cs.r1 = make_rsrc(W1h + (size_t)c * 32, D * E * 2 - 64 * c);
-    cs.r2 = make_rsrc(W2h + (size_t)c * 32 * D, clamp0(cs.lim, 32) * D * 2);
-    return cs;
-  };
-  auto load_piece = [&](const ChunkSrc& cs, int k) {
-    if (k < PPT / 2) stg[k] = buf_load16(cs.r1, (int)colq < cs.lim ? offW1g[k] : BUF_OOB);
-    else stg[k] = buf_load16(cs.r2, offW2g[k - PPT / 2]);
-  };
-  auto store_piece = [&](int slot, int k) {
-    const unsigned base = slot * SLOT;
-    const unsigned p = tid + (k % (PPT / 2)) * NT;
-    if (k < PPT / 2) lds_write16(base + p * 16u, stg[k]);  // d*64 + q*16
-    else lds_write16(base + W2OFF + (p >> 7) * 2048u + ((p >> 2) & 31u) * 64u + (p & 3u) * 16u, stg[k]);
-  };
-  auto load_chunk = [&](int c) {
-    const ChunkSrc cs = chunk_src(c);
-#pragma unroll
-    for (int k = 0; k < PPT; ++k) load_piece(cs, k);
-  };
-  auto store_chunk = [&](int slot) {
-#pragma unroll
-    for (int k = 0; k < PPT; ++k) store_piece(slot, k);
+  // ---- chunk staging: buffer-to-LDS loads, PF chunks ahead into an NSLOT-slot ring ----
+  // One 16-byte piece per thread per region (NT == 4 D): piece p = tid of W1c lands at slot
+  // offset 16 p (row d = p / 4, columns 8 (p % 4) ..), piece p of W2c at W2OFF + 16 p (block
+  // p / 128, row (p / 4) % 32, columns 32 (p / 128) + 8 (p % 4) ..). Columns past E (and every
+  // piece of a chunk past the last) are out of range and land as zeros.
+  static_assert(NT == 4 * D, "one piece per thread per region");
+  const int colq = (tid & 3) * 8;
+  const unsigned dOffW1 = (unsigned)(tid >> 2) * (unsigned)E * 2u + (tid & 3u) * 16u;
+  const unsigned dOffW2 = ((tid >> 2) & 31u) * (D * 2u) + (unsigned)(tid >> 7) * 64u + (tid & 3u) * 16u;
+  auto dma_chunk = [&](int c) {
+    const int lim = E - c * 32;
+    const int rem = D * E * 2 - 64 * c;
+    const i32x4 r1 = make_rsrc_words(W1h + (size_t)c * 32, rem > 0 ? rem : 0);
+    const i32x4 r2 = make_rsrc_words(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
+    const int slot = (c & (NSLOT - 1)) * (int)SLOT + wave * 1024;
+    buf_load16_lds(r1, colq < lim ? dOffW1 : BUF_OOB, slot);
+    buf_load16_lds(r2, dOffW2, slot + (int)W2OFF);
   };
   // end of a chunk: the LDS stores are retired and visible after the barrier; the loads of
   // the chunk after next stay in flight (their data is waited for where it is stored)
   auto chunk_end = [&]() {
+    wait_vmcnt<2 * (PF - 2)>();          // this wave's pieces of the chunk read next
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -133,13 +121,8 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   for (int nt = 0; nt < NTN; ++nt) o[nt] = zero16();
 
   // ---- prologue: chunks 0 and 1 in LDS, chunk 2 in registers, Z^T(0) ----
-  load_chunk(0);
-  store_chunk(0);
-  if (NC > 1) {
-    load_chunk(1);
-    store_chunk(1);
-  }
-  load_chunk(2);
+#pragma unroll
+  for (int c = 0; c < PF; ++c) dma_chunk(c);
   chunk_end();
   // Pipeline state carried between iterations: Z^T of the chunk to activate and h of the
   // previous chunk (A operand of O += h W2c, two K steps). Iterations run in pairs with the
@@ -162,14 +145,12 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     constexpr bool DO_G2 = decltype(G2)::value;
     constexpr int N1 = DO_G1 ? KS : 0, N2 = DO_G2 ? KS : 0, NOPS = N1 + N2;
     constexpr int PER = 16 / NOPS;  // activation elements per step
-    const unsigned base1 = ((c + 1) & 3) * SLOT, base2 = ((c - 1) & 3) * SLOT;
+    const unsigned base1 = ((c + 1) & (NSLOT - 1)) * SLOT, base2 = ((c - 1) & (NSLOT - 1)) * SLOT;
 
     // chunk c+2 (loaded during iteration c-1) goes to its slot and chunk c+3 is loaded into
     // the same registers, one 16-byte piece per step (store of piece k at step 2k, its next
     // load at step 2k+1)
-    const int sslot = (c + 2) & 3;
-    const ChunkSrc cs = chunk_src(c + 3);
-    static_assert(2 * PPT <= KS, "staging steps");
+    dma_chunk(c + PF);
 
     // op j: G1 and G2 alternate when both are present
     auto is_g1 = [&](int j) { return DO_G1 && (!DO_G2 || (j % 2 == 0)); };
@@ -178,20 +159,16 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       const int k = idx(j);
       return is_g1(j) ? opndA(base1, k) : opndB(base2, k / NTN, k % NTN);
     };
-    u32x4 op0 = fetch(0), op1 = NOPS > 1 ? fetch(1) : op0, op2 = op0;
+    constexpr int PDX = NOPS < 2 ? NOPS : 2;  // operand reads two steps ahead
+    u32x4 ring[PDX + 1];
+#pragma unroll
+    for (int j = 0; j < PDX; ++j) ring[j] = fetch(j);
     float hv[16];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NOPS; ++j) {
-      const u32x4 cur = (j % 3 == 0) ? op0 : (j % 3 == 1) ? op1 : op2;
-      if (j + 2 < NOPS) {
-        const u32x4 nx = fetch(j + 2);
-        if ((j + 2) % 3 == 0) op0 = nx; else if ((j + 2) % 3 == 1) op1 = nx; else op2 = nx;
-      }
-      if (j < 2 * PPT) {
-        if ((j & 1) == 0) store_piece(sslot, j >> 1);
-        else load_piece(cs, j >> 1);
-      }
+      const u32x4 cur = ring[j % (PDX + 1)];
+      if (j + PDX < NOPS) ring[(j + PDX) % (PDX + 1)] = fetch(j + PDX);
       const int k = idx(j);
       if (is_g1(j)) {  // k == 0 starts the chain from a literal zero accumulator
         out.z = mfma<BF16>(cur, xr[k], k == 0 ? zero16() : out.z);
@@ -214,7 +191,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     chunk_end();
   };
   auto last_gemm2 = [&](const St& st) {
-    const unsigned base2 = ((NC - 1) & 3) * SLOT;
+    const unsigned base2 = ((NC - 1) & (NSLOT - 1)) * SLOT;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -246,6 +223,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     }
   }
 
+  wait_vmcnt<0>();  // chunks past the last are still landing (as zeros)
   // ---- epilogue: O tile (C layout: lane = column d, rows 8(i/4) + 4g + i%4); fp32 sums
   // when the caller asked for them (FMLP_OUT_F32), else rounded to the io dtype ----
   if (outf32) {
@@ -276,16 +254,16 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 // ------------------------------------------------------------------------------------
 template <bool BF16, int D, int ACT>
 static hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t st) {
-  constexpr int BB = 128;
+  constexpr int BB = 32 * fwd_waves(D);
   const int tiles_per_head = (int)((a.B + BB - 1) / BB);
   const long long grid = (long long)tiles_per_head * a.H;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  const size_t lds = 4u * 128u * D;
+  const size_t lds = (size_t)FWD_NSLOT * 128u * D;
   auto k = fwd_kernel<BF16, D, ACT>;
   hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(256), lds, st, (const u16*)a.x, (const u16*)a.w1,
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(64 * fwd_waves(D)), lds, st, (const u16*)a.x, (const u16*)a.w1,
                      (const u16*)a.w2, a.o, (int)a.B, (int)a.E, tiles_per_head, a.out_f32 ? 1 : 0);
   return hipGetLastError();
 }
