@@ -575,8 +575,8 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     valu_phase();
     chunk_end();
     for (int c = 1; c < NC; ++c) {
-      chunk_begin(c);
       mfma_phase(T, c);
+      chunk_begin(c);  // staged between the phases: fewer LDS writes next to the operand reads
       valu_phase();
       chunk_end();
     }

@@ -195,7 +195,12 @@ class FlashMLP(torch.nn.Module):
         else:
             squeeze_output = False
 
-        o = FlashMLPFunction.apply(x, self.w1, self.w2, self.activation)
+        if torch.compiler.is_compiling():
+            # the registered operator (flashmlp_amd.ops) is what torch.compile traces through
+            from .ops import flashmlp as _op
+            o = _op(x, self.w1, self.w2, self.activation)
+        else:
+            o = FlashMLPFunction.apply(x, self.w1, self.w2, self.activation)
 
         if squeeze_output:
             o = o.mean(dim=0)
