@@ -3,21 +3,29 @@
     python bench.py [--steps K] [--warmup W] [--workload cfg4]
 
 A step is one flashmlp_fwd + flashmlp_bwd over the workload's synthetic inputs, all
-resident in HBM before the timed region. Prints ONE JSON line (rank 0 of one process).
+resident in HBM before the timed region (cfg5s: one flashmlp_fwd, the forward-only sweep).
+Prints ONE JSON line (one process, one GPU).
 
 FLOP accounting: u = H*B*D*E; forward 4u, backward 8u, step 12u.
-`value` = 12u / wall-clock ms_per_step. `roofline` describes the dominant launch, the
-backward entry point fmlp_bwd (its dW and dX kernels, 8u algorithmic FLOPs per call),
-with its duration from HIP events recorded on the stream the kernels run on; the
-per-kernel split is in the committed rocprofv3 summary. `cpu_baseline` times the CPU
-oracle (torch fp32 autograd of the restated reference path) on a bounded sample of the
-same workload.
+`value` = 12u / wall-clock ms_per_step (4u for cfg5s). `roofline` describes the dominant
+launch, the backward entry point fmlp_bwd (8u algorithmic FLOPs per call; the forward for
+cfg5s), with its duration from HIP events recorded on the stream the kernels run on.
+Algorithmic HBM bytes at s bytes per element: forward (2 HBD + 2 HDE) s, backward
+(3 HBD + 4 HDE) s. `autograd_ms_per_step` times the module-level step the reference's
+example.py:120-128 times (FlashMLPFunction forward, then .backward). `cpu_baseline` times
+the CPU oracle (torch fp32 autograd of the restated reference path) on a bounded sample of
+the same workload, plus the reference's CPU configuration (cfg1) in full.
+
+Other workloads: cfg2, cfg3, cfg5, cfg5_linear (fwd+bwd), cfg5s
+(forward-only, reports HBM GB/s), example (the four shapes of the reference's
+performance.md through the FlashMLP module, timed as example.py times them).
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -30,11 +38,19 @@ PEAK_TFLOPS = {"bf16": 2516.6, "f16": 2516.6}  # MI355X dense MFMA, 256 CU x 2.4
 HBM_GBS = 8000.0
 
 WORKLOADS = {
-    # name: (H, B, D, E, dtype, activation, x_std)
-    "cfg4": (32, 16384, 128, 1024, "bf16", "silu", 1.0),
-    "cfg3": (16, 8192, 128, 512, "bf16", "leaky_relu", 1.0),
-    "cfg2": (12, 1024, 64, 768, "f16", "silu", 1.0),
-    "cfg5": (8, 4097, 64, 2048, "f16", "sigmoid", 2.0),
+    # name: (H, B, D, E, dtype, activation, x_std, forward_only)
+    "cfg4": (32, 16384, 128, 1024, "bf16", "silu", 1.0, False),
+    "cfg3": (16, 8192, 128, 512, "bf16", "leaky_relu", 1.0, False),
+    "cfg2": (12, 1024, 64, 768, "f16", "silu", 1.0, False),
+    "cfg5": (8, 4097, 64, 2048, "f16", "sigmoid", 2.0, False),
+    "cfg5_linear": (8, 4097, 64, 2048, "f16", "", 2.0, False),
+    "cfg5s": (8, 65536, 64, 2048, "f16", "sigmoid", 2.0, True),
+}
+# performance.md:9-12 (example.py:86-91): bf16, SiLU, timed through the FlashMLP module
+EXAMPLE_SHAPES = [(8, 512, 64, 512), (12, 1024, 64, 768), (16, 2048, 64, 1024), (32, 4096, 64, 512)]
+EXAMPLE_PUBLISHED_MS = {  # (fwd, fwd+bwd) of the reference on its (unstated) hardware
+    (8, 512, 64, 512): (0.036, 0.217), (12, 1024, 64, 768): (0.035, 0.222),
+    (16, 2048, 64, 1024): (0.036, 0.219), (32, 4096, 64, 512): (0.060, 0.380),
 }
 
 
@@ -58,49 +74,71 @@ def make_gpu_inputs(H, B, D, E, dtype, x_std, seed=0):
     return x, w1, w2, do
 
 
-def traffic_from_profile(workload):
-    """HBM bytes per backward call (dW + dX kernels) from the committed rocprofv3 PMC
-    summary (FETCH_SIZE and WRITE_SIZE runs, each scaled by the same counter's reading for
-    a device copy of known size), or None when no summary exists for this workload."""
-    path = os.path.join(ROOT, "profiles", f"bwd_{workload}_traffic.txt")
+def traffic_from_profile(kind, workload):
+    """HBM bytes per call of the `kind` entry point ("bwd" or "fwd") from the committed
+    rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE runs, each scaled by the same counter's
+    reading for a device copy of known size), or None when no summary exists."""
+    path = os.path.join(ROOT, "profiles", f"{kind}_{workload}_traffic.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
         for line in f:
             key, _, val = line.partition("=")
-            if key.strip() == "hbm_bytes_per_call_bwd":
+            if key.strip() == f"hbm_bytes_per_call_{kind}":
                 return int(float(val))
     return None
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(H, B, D, E, activation, x_std, budget_s=10.0):
-    """Torch fp32 autograd of the restated reference path on the host cores, on a sample of
-    the workload: 2 of the H heads (heads are independent), full B, D, E."""
+    """Torch fp32 autograd of the restated reference path on the host cores this process may
+    run on: a bounded sample of the workload (2 of the H heads, heads being independent,
+    full B, D, E; about `budget_s` of work), and the reference's CPU configuration cfg1
+    (H=12 B=1024 D=64 E=768 SiLU) in full, median of 20 iterations."""
     import torch
 
     from oracle import reference
-    from oracle.inputs import make_inputs
+    from oracle.inputs import CONFIGS, make_inputs
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+
+    def timed(args, act, min_iter, budget):
+        reference.autograd_grads(*args, act)  # warm-up
+        ts = []
+        t_end = time.perf_counter() + budget
+        while len(ts) < min_iter or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            reference.autograd_grads(*args, act)
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts), len(ts)
 
     hs = min(2, H)
-    x, w1, w2, do = make_inputs(hs, B, D, E, torch.float32, x_std, seed=0)
-    threads = torch.get_num_threads()
-    reference.autograd_grads(x, w1, w2, do, activation)  # warm-up
-    n = 0
-    t0 = time.perf_counter()
-    while True:
-        reference.autograd_grads(x, w1, w2, do, activation)
-        n += 1
-        if time.perf_counter() - t0 >= budget_s:
-            break
-    dt = (time.perf_counter() - t0) / n
-    flops = 12.0 * hs * B * D * E
+    dt, n = timed(make_inputs(hs, B, D, E, torch.float32, x_std, seed=0), activation, 3, budget_s)
+    c1 = CONFIGS["cfg1"]
+    dt1, n1 = timed(make_inputs(c1.H, c1.B, c1.D, c1.E, torch.float32, c1.x_std, seed=0), c1.activation, 20, 0.0)
+    u1 = float(c1.H) * c1.B * c1.D * c1.E
     return {
-        "value": flops / dt / 1e12,
+        "value": 12.0 * hs * B * D * E / dt / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{hs} of {H} heads (H={hs},B={B},D={D},E={E}, fp32, {activation}), "
-                  f"fwd + autograd bwd, {n} iterations, {dt * 1e3:.1f} ms each",
+        "cpu_model": _cpu_model(),
+        "sample": f"{hs} of {H} heads (H={hs},B={B},D={D},E={E}, fp32, {activation or 'linear'}), "
+                  f"fwd + autograd bwd, median of {n} iterations, {dt * 1e3:.1f} ms each",
+        "cfg1_ms": round(dt1 * 1e3, 3),
+        "cfg1_gflops": round(12 * u1 / dt1 / 1e9, 1),
+        "cfg1": f"H={c1.H} B={c1.B} D={c1.D} E={c1.E} fp32 {c1.activation}, median of {n1} iterations",
     }
 
 
@@ -160,14 +198,98 @@ def peak_memory(x, w1, w2, do, activation):
     return out
 
 
+def _wall_ms(fn, iters):
+    """example.py:65-75: perf_counter around `iters` calls, synchronised at both ends."""
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / iters * 1e3
+
+
+def host_us_per_call(fn, n=200):
+    """CPU time to issue one call (Python wrapper + C ABI + launch), measured with the GPU
+    idle so the launch queue never blocks: mean over n issues, then synchronise."""
+    import torch
+
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(n):
+        fn()
+    t1 = time.perf_counter()
+    torch.cuda.synchronize()
+    return (t1 - t0) / n * 1e6
+
+
+def autograd_step_ms(x, w1, w2, do, act, warmup=3, iters=20):
+    """Module-level training step as example.py:120-128 times it: FlashMLPFunction forward
+    on a leaf that requires grad, then backward (here with dO, the bench's gradient)."""
+    import flashmlp_amd as fm
+
+    xg = x.detach().requires_grad_(True)
+    w1g = w1.detach().requires_grad_(True)
+    w2g = w2.detach().requires_grad_(True)
+
+    def step():
+        o = fm.FlashMLPFunction.apply(xg, w1g, w2g, act)
+        o.backward(do)
+        xg.grad = w1g.grad = w2g.grad = None
+
+    for _ in range(warmup):
+        step()
+    return _wall_ms(step, iters)
+
+
+def run_example(args):
+    """performance.md's four shapes through the FlashMLP module, timed like example.py
+    (10 warmup + 100 iterations, wall clock, fwd = model(x), fwd+bwd = model(x).sum().backward())."""
+    import numpy as np
+    import torch
+
+    import flashmlp_amd as fm
+
+    rows = []
+    for H, B, D, E in EXAMPLE_SHAPES:
+        torch.manual_seed(0)
+        model = fm.FlashMLP(H, D, E, activation="silu", dtype=torch.bfloat16, device="cuda")
+        x = torch.randn(H, B, D, device="cuda", dtype=torch.bfloat16) / np.sqrt(D)
+
+        def fwd():
+            return model(x)
+
+        def fwd_bwd():
+            x_in = x.detach().requires_grad_(True)
+            model(x_in).sum().backward()
+
+        for f in (fwd, fwd_bwd):
+            for _ in range(10):
+                f()
+        t_f = _wall_ms(fwd, 100)
+        t_fb = _wall_ms(fwd_bwd, 100)
+        u = float(H) * B * D * E
+        pub = EXAMPLE_PUBLISHED_MS[(H, B, D, E)]
+        rows.append({"H": H, "B": B, "D": D, "E": E, "fwd_ms": round(t_f, 4), "fwd_bwd_ms": round(t_fb, 4),
+                     "fwd_tflops": round(4 * u / t_f / 1e9, 2), "fwd_bwd_tflops": round(12 * u / t_fb / 1e9, 2),
+                     "reference_published_ms": {"fwd": pub[0], "fwd_bwd": pub[1], "hardware": "unstated"}})
+        model.zero_grad()
+    line = {"metric": METRIC, "workload": "example", "unit": "ms", "dtype": "bf16",
+            "note": "performance.md shapes through FlashMLP (module, autograd), wall clock incl. Python",
+            "rows": rows}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="cfg4", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="cfg4", choices=sorted(WORKLOADS) + ["example"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-memory", action="store_true", help="skip the peak-memory comparison")
+    ap.add_argument("--no-extra", action="store_true", help="skip the autograd-step and host-overhead timings")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="after timing, run device copies of this size (HBM counter calibration)")
     args = ap.parse_args()
@@ -183,19 +305,21 @@ def main():
 
     import flashmlp_amd as fm
 
-    H, B, D, E, dt_name, act, x_std = WORKLOADS[args.workload]
-    dtype = _torch_dtype(dt_name)
     torch.cuda.set_device(0)
+    if args.workload == "example":
+        run_example(args)
+        return
+
+    H, B, D, E, dt_name, act, x_std, fwd_only = WORKLOADS[args.workload]
+    dtype = _torch_dtype(dt_name)
     x, w1, w2, do = make_gpu_inputs(H, B, D, E, dtype, x_std)
     torch.cuda.synchronize()
-
-    def step():
-        o = fm.flashmlp_fwd(x, w1, w2, act)
-        g = fm.flashmlp_bwd(x, w1, w2, do, act)
-        return o, g
+    s = 2  # bytes per io element
 
     for _ in range(args.warmup):
-        step()
+        fm.flashmlp_fwd(x, w1, w2, act)
+        if not fwd_only:
+            fm.flashmlp_bwd(x, w1, w2, do, act)
     torch.cuda.synchronize()
 
     K = args.steps
@@ -206,20 +330,25 @@ def main():
         ev[k][0].record()
         o = fm.flashmlp_fwd(x, w1, w2, act)
         ev[k][1].record()
-        g = fm.flashmlp_bwd(x, w1, w2, do, act)
+        if not fwd_only:
+            g = fm.flashmlp_bwd(x, w1, w2, do, act)
         ev[k][2].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / K
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K
-    assert torch.isfinite(o.float()).all() and all(torch.isfinite(t.float()).all() for t in g)
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K if not fwd_only else 0.0
+    assert torch.isfinite(o.float()).all()
+    if not fwd_only:
+        assert all(torch.isfinite(t.float()).all() for t in g)
 
     u = float(H) * B * D * E
+    flops = (4 if fwd_only else 12) * u
     ms_per_step = wall * 1e3 / K
-    value = 12 * u / (ms_per_step * 1e-3) / 1e12
+    value = flops / (ms_per_step * 1e-3) / 1e12
     peak = PEAK_TFLOPS[dt_name]
-    bwd_tf = 8 * u / (bwd_ms * 1e-3) / 1e12
     fwd_tf = 4 * u / (fwd_ms * 1e-3) / 1e12
+    fwd_bytes = (2 * H * B * D + 2 * H * D * E) * s
+    bwd_bytes = (3 * H * B * D + 4 * H * D * E) * s
 
     if args.calib_copy_mb > 0:
         n = args.calib_copy_mb * 2 ** 20 // 4
@@ -230,6 +359,7 @@ def main():
         torch.cuda.synchronize()
         del src, dst
 
+    step_name = "fused MLP forward (inference sweep)" if fwd_only else "fused MLP fwd+bwd"
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -242,27 +372,52 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": dt_name,
-        "data": "synthetic (seeded N(0,1) X and dO, N(0,1/D) W1, N(0,1/E) W2, drawn on the GPU)",
-        "config": {"workload": f"{args.workload}: fused MLP fwd+bwd H={H} B={B} D={D} E={E} act={act or 'linear'}",
-                   "H": H, "B": B, "D": D, "E": E, "activation": act, "flops_per_step": 12 * u},
+        "data": f"synthetic (seeded N(0,{x_std:g}^2) X, N(0,1) dO, N(0,1/D) W1, N(0,1/E) W2, drawn on the GPU)",
+        "config": {"workload": f"{args.workload}: {step_name} H={H} B={B} D={D} E={E} act={act or 'linear'}",
+                   "H": H, "B": B, "D": D, "E": E, "activation": act, "flops_per_step": flops},
         "pct_of_peak": round(100 * value / peak, 2),
         "fwd_ms": round(fwd_ms, 4),
-        "bwd_ms": round(bwd_ms, 4),
         "fwd_tflops": round(fwd_tf, 2),
-        "bwd_tflops": round(bwd_tf, 2),
-        "roofline": {
+        "fwd_hbm_gbs": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9, 1),
+    }
+    if fwd_only:
+        line["roofline"] = {
+            "kernel": "fmlp_fwd call: fmlp::fwd_kernel",
+            "bound": "mfma",
+            "achieved": round(fwd_tf, 2),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(fwd_tf / peak, 4),
+            "traffic": traffic_from_profile("fwd", args.workload),
+            "algorithmic_flops_per_launch": 4 * u,
+            "algorithmic_bytes_per_launch": fwd_bytes,
+            "avg_launch_ms": round(fwd_ms, 4),
+            "hbm_gbs": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9, 1),
+            "hbm_frac": round(fwd_bytes / (fwd_ms * 1e-3) / 1e9 / HBM_GBS, 4),
+        }
+    else:
+        bwd_tf = 8 * u / (bwd_ms * 1e-3) / 1e12
+        line["bwd_ms"] = round(bwd_ms, 4)
+        line["bwd_tflops"] = round(bwd_tf, 2)
+        line["bwd_hbm_gbs"] = round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1)
+        line["roofline"] = {
             "kernel": "fmlp_bwd call: fmlp::dw2_kernel + fmlp::dx2_kernel",
             "bound": "mfma",
             "achieved": round(bwd_tf, 2),
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(bwd_tf / peak, 4),
-            "traffic": traffic_from_profile(args.workload),
+            "traffic": traffic_from_profile("bwd", args.workload),
             "algorithmic_flops_per_launch": 8 * u,
+            "algorithmic_bytes_per_launch": bwd_bytes,
             "avg_launch_ms": round(bwd_ms, 4),
-        },
-    }
-    if not args.no_memory:
+        }
+    if not args.no_extra:
+        line["host_us_per_call"] = {"fwd": round(host_us_per_call(lambda: fm.flashmlp_fwd(x, w1, w2, act)), 2)}
+        if not fwd_only:
+            line["host_us_per_call"]["bwd"] = round(host_us_per_call(lambda: fm.flashmlp_bwd(x, w1, w2, do, act)), 2)
+            line["autograd_ms_per_step"] = round(autograd_step_ms(x, w1, w2, do, act), 4)
+    if not args.no_memory and not fwd_only:
         line["memory"] = peak_memory(x, w1, w2, do, act)
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(H, B, D, E, act, x_std)

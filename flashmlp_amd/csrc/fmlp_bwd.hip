@@ -20,8 +20,8 @@ namespace fmlp {
 
 constexpr int DW_ET = 128;           // E columns per dW program (32 per wave column group)
 constexpr int DW_BT = 32;            // rows per streamed subtile
-// dX workgroups of the 4-wave form: 128 rows.
-__host__ __device__ constexpr int dx_waves(int D) { return D > 0 ? 4 : 4; }
+// dX workgroups of the 4-wave form (one wave per SIMD): 128 rows.
+constexpr int DX_WAVES = 4;
 
 // dW epilogue. C layout of the accumulators: lane = column d
 // (32 nt + l32), rows e = e0 + 8 (i / 4) + 4 g + (i % 4). nS == 1 writes dW1, dW2 in the io
@@ -872,11 +872,11 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 // dX programs: 4 waves; at D = 64 two workgroups share a CU (two waves per SIMD), at
 // D = 128 the role needs more than 256 VGPRs and runs one wave per SIMD.
 template <bool BF16, int D, int ACT, int MT>
-__global__ void __launch_bounds__(dx_waves(D) * 64)
+__global__ void __launch_bounds__(DX_WAVES * 64)
 dx_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
           const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
-  dx_role<BF16, D, ACT, MT, dx_waves(D)>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32,
-                                         xcd_remap(blockIdx.x, gridDim.x));
+  dx_role<BF16, D, ACT, MT, DX_WAVES>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32,
+                                      xcd_remap(blockIdx.x, gridDim.x));
 }
 
 // Sum of the nS fp32 partials; dW2 keeps the (e, d) layout, dW1 is written transposed.
@@ -923,14 +923,14 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus) {
   if (ns < 1) ns = 1;
   p.nS = (int)ns;
   p.rows_per_split = (int)rps;
-  // dX programs: 256 rows when that still gives >= 2 programs per CU, else 128
-  // (D = 128 with two M-tiles per wave exceeds the register file, so it keeps one)
   // dX programs: the 8-wave form unless it would leave most CUs idle (measured on MI355X:
-  // it wins from about a quarter of the CUs busy, the 4-wave form below that)
+  // it wins from about a quarter of the CUs busy, the 4-wave form below that).
+  // FMLP_DX_KIND (read once per process) forces 0 (4-wave) or 1 (8-wave).
+  static const int dx_kind_env = env_int("FMLP_DX_KIND", -1);
   const long long big = (B + DX2_ROWS - 1) / DX2_ROWS * H;
   p.dx_mt = 1;
-  p.dx_kind = env_int("FMLP_DX_KIND", 4 * big >= num_cus ? 1 : 0) ? 1 : 0;
-  const int rows = p.dx_kind ? DX2_ROWS : dx_waves((int)D) * 32 * p.dx_mt;
+  p.dx_kind = dx_kind_env >= 0 ? (dx_kind_env ? 1 : 0) : (4 * big >= num_cus ? 1 : 0);
+  const int rows = p.dx_kind ? DX2_ROWS : DX_WAVES * 32 * p.dx_mt;
   p.dx_tiles_per_head = (int)((B + rows - 1) / rows);
   p.n_dw = base * p.nS;
   p.n_dx = (long long)p.dx_tiles_per_head * H;
@@ -946,7 +946,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   if (p.n_dw > 0) {
     const size_t lds = 1280u * D;  // two weight tiles (256 D bytes each) + three subtile pairs (256 D each)
     auto k = dw2_kernel<BF16, D, ACT>;
-    e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    static std::atomic<unsigned long long> lds_set{0};
+    e = set_lds_once((const void*)k, (int)lds, lds_set);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
                        (const u16*)a.w2, (const u16*)a.dout, a.dw1, a.dw2, (float*)a.ws, (int)a.H,
@@ -966,9 +967,10 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   if (p.n_dx > 0) {
     const size_t lds = 4u * 128u * D;
     auto launch = [&](auto k) {
-      hipError_t r = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      static std::atomic<unsigned long long> lds_set{0};
+      hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
       if (r != hipSuccess) return r;
-      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(dx_waves(D) * 64), lds, st, (const u16*)a.x, (const u16*)a.w1,
+      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(DX_WAVES * 64), lds, st, (const u16*)a.x, (const u16*)a.w1,
                          (const u16*)a.w2, (const u16*)a.dout, a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head,
                          a.out_f32 ? 1 : 0);
       return hipGetLastError();
@@ -976,7 +978,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     if (p.dx_kind == 1) {
       const size_t lds2 = 4u * 128u * D;
       auto k = dx2_kernel<BF16, D, ACT>;
-      e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds2);
+      static std::atomic<unsigned long long> lds_set{0};
+      e = set_lds_once((const void*)k, (int)lds2, lds_set);
       if (e != hipSuccess) return e;
       hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(DX2_NT), lds2, st, (const u16*)a.x, (const u16*)a.w1,
                          (const u16*)a.w2, (const u16*)a.dout, a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head,

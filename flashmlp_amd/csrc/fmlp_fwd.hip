@@ -58,10 +58,6 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const u16* W2h = W2 + (size_t)h * E * D;
   const int b_wave = bt * BB + wave * 32;
 
-  // ---- chunk staging: global -> registers (one chunk ahead) -> LDS ----
-  // Branch-free buffer loads: W2c rows past E fall outside the chunk's resource; W1c
-  // columns past E (last chunk when E % 32 != 0) get an out-of-range offset. Chunks past
-  // the last one are loaded but never used.
   // ---- chunk staging: buffer-to-LDS loads, PF chunks ahead into an NSLOT-slot ring ----
   // One 16-byte piece per thread per region (NT == 4 D): piece p = tid of W1c lands at slot
   // offset 16 p (row d = p / 4, columns 8 (p % 4) ..), piece p of W2c at W2OFF + 16 p (block
@@ -120,7 +116,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 #pragma unroll
   for (int nt = 0; nt < NTN; ++nt) o[nt] = zero16();
 
-  // ---- prologue: chunks 0 and 1 in LDS, chunk 2 in registers, Z^T(0) ----
+  // ---- prologue: chunks 0 .. PF-1 requested, chunk 0 waited for, Z^T(0) ----
 #pragma unroll
   for (int c = 0; c < PF; ++c) dma_chunk(c);
   chunk_end();
@@ -147,9 +143,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     constexpr int PER = 16 / NOPS;  // activation elements per step
     const unsigned base1 = ((c + 1) & (NSLOT - 1)) * SLOT, base2 = ((c - 1) & (NSLOT - 1)) * SLOT;
 
-    // chunk c+2 (loaded during iteration c-1) goes to its slot and chunk c+3 is loaded into
-    // the same registers, one 16-byte piece per step (store of piece k at step 2k, its next
-    // load at step 2k+1)
+    // chunk c+PF is requested straight into its LDS slot (PF chunks ahead of the one read)
     dma_chunk(c + PF);
 
     // op j: G1 and G2 alternate when both are present
@@ -261,26 +255,21 @@ static hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
   const size_t lds = (size_t)FWD_NSLOT * 128u * D;
   auto k = fwd_kernel<BF16, D, ACT>;
-  hipError_t e = hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  static std::atomic<unsigned long long> lds_set{0};
+  hipError_t e = set_lds_once((const void*)k, (int)lds, lds_set);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(64 * fwd_waves(D)), lds, st, (const u16*)a.x, (const u16*)a.w1,
                      (const u16*)a.w2, a.o, (int)a.B, (int)a.E, tiles_per_head, a.out_f32 ? 1 : 0);
   return hipGetLastError();
 }
 
-template <bool BF16, int D, int ACT>
-static hipError_t launch_fwd_d(const FwdArgs& a, hipStream_t st) {
-  // 4 waves x 32 rows per workgroup; two workgroups share a CU (two waves per SIMD)
-  return launch_fwd_t<BF16, D, ACT>(a, st);
-}
-
 template <bool BF16, int D>
 static hipError_t launch_fwd_a(const FwdArgs& a, hipStream_t st) {
   switch (a.act) {
-    case ACT_SILU: return launch_fwd_d<BF16, D, ACT_SILU>(a, st);
-    case ACT_LEAKY: return launch_fwd_d<BF16, D, ACT_LEAKY>(a, st);
-    case ACT_SIGMOID: return launch_fwd_d<BF16, D, ACT_SIGMOID>(a, st);
-    default: return launch_fwd_d<BF16, D, ACT_NONE>(a, st);
+    case ACT_SILU: return launch_fwd_t<BF16, D, ACT_SILU>(a, st);
+    case ACT_LEAKY: return launch_fwd_t<BF16, D, ACT_LEAKY>(a, st);
+    case ACT_SIGMOID: return launch_fwd_t<BF16, D, ACT_SIGMOID>(a, st);
+    default: return launch_fwd_t<BF16, D, ACT_NONE>(a, st);
   }
 }
 

@@ -4,10 +4,17 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace fmlp {
 
 // Integer tuning override from the environment (tile shapes); `dflt` when unset.
 int env_int(const char* name, int dflt);
+
+// Raises `kernel`'s dynamic-LDS limit to `bytes` on the current device, once per device:
+// `done` is the caller's per-kernel flag word (bit = device ordinal), so later launches
+// skip the runtime call.
+hipError_t set_lds_once(const void* kernel, int bytes, std::atomic<unsigned long long>& done);
 
 struct FwdArgs {
   const void* x;

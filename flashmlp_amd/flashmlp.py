@@ -23,6 +23,7 @@ Differences from the reference, all deliberate:
 """
 from __future__ import annotations
 
+import functools
 from typing import Tuple
 
 import numpy as np
@@ -51,6 +52,13 @@ def _check_tensors(*ts: torch.Tensor) -> int:
         if t.dtype != dt:
             raise TypeError(f"all tensors must share one dtype ({dt} vs {t.dtype})")
     return _DTYPES[dt]
+
+
+@functools.lru_cache(maxsize=256)
+def _ws_bytes(device_index: int, H: int, B: int, D: int, E: int, dtype: int) -> int:
+    # the backward plan depends only on the shapes and the device's CU count; asked once per
+    # (device, shape) so a call plans the backward only inside fmlp_bwd itself
+    return int(_lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, dtype))
 
 
 def _aligned(t: torch.Tensor) -> torch.Tensor:
@@ -130,7 +138,8 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     dw2 = torch.empty_like(w2)
     L = _lib.lib()
     with torch.cuda.device(x.device):
-        ws_bytes = int(L.fmlp_bwd_workspace_bytes(H, B, D, E, dtype))
+        ws_bytes = _ws_bytes(x.device.index if x.device.index is not None else torch.cuda.current_device(),
+                             H, B, D, E, dtype)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
         stream = torch.cuda.current_stream(x.device).cuda_stream
         st = L.fmlp_bwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(), dw1.data_ptr(),

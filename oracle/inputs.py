@@ -32,7 +32,8 @@ CONFIGS = {
     "cfg4": Config("cfg4", 32, 16384, 128, 1024, torch.bfloat16, "silu"),
     "cfg5_linear": Config("cfg5_linear", 8, 4097, 64, 2048, torch.float16, "", 2.0),
     "cfg5_sigmoid": Config("cfg5_sigmoid", 8, 4097, 64, 2048, torch.float16, "sigmoid", 2.0),
-    "cfg5s": Config("cfg5s", 8, 65536, 64, 2048, torch.float16, "silu", 2.0),
+    # forward-only inference sweep of config 5 at B = 65536 (sigmoid; the tests also run linear)
+    "cfg5s": Config("cfg5s", 8, 65536, 64, 2048, torch.float16, "sigmoid", 2.0),
 }
 
 

@@ -108,3 +108,22 @@ def test_split_reduction_sums():
 def test_config_sums(name):
     c = CONFIGS[name]
     run_sums(name, c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=[0, c.H - 1])
+
+
+def test_config5s_forward_sums():
+    # the B = 65536 forward-only sweep: the forward's fp32 sums only
+    c = CONFIGS["cfg5s"]
+    x, w1, w2, _ = make_inputs(c.H, c.B, c.D, c.E, c.dtype, c.x_std, seed=0, with_do=False)
+    _say(f"[fp32-sums] cfg5s forward: H={c.H} B={c.B} D={c.D} E={c.E} {c.dtype} act='{c.activation}'")
+    L = _lib.lib()
+    xd, w1d, w2d = (t.cuda() for t in (x, w1, w2))
+    o = torch.empty(c.H, c.B, c.D, dtype=torch.float32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    _lib.check(L.fmlp_fwd(_ptr(xd), _ptr(w1d), _ptr(w2d), _ptr(o), c.H, c.B, c.D, c.E,
+                          _DT[c.dtype] | _lib.FMLP_OUT_F32, _lib.ACT_CODES[c.activation], stream), "fp32-sum forward")
+    torch.cuda.synchronize()
+    hs = [0, c.H - 1]
+    eo = emulate.emu_fwd(x[hs], w1[hs], w2[hs], c.activation, c.dtype, round_out=False)
+    rel = _normrel(o[hs].cpu(), eo)
+    _say(f"[fp32-sums] cfg5s forward: o_rel={rel:.3g}")
+    assert rel <= BAR

@@ -1,12 +1,14 @@
 """The registered operators on the GPU: torch.library.opcheck (schema, fake kernel against
-the real one, autograd registration, AOT dispatch) and torch.compile through AOTAutograd
-(backend "aot_eager", so the compiled graph runs the same HIP kernels) against eager."""
+the real one, autograd registration, AOT dispatch), torch.compile through AOTAutograd
+(backend "aot_eager", so the compiled graph runs the same HIP kernels) against eager, and
+the compiled operator path against the CPU oracle at the parity bars of test_gpu_parity."""
 import sys
 
 import pytest
 import torch
 
 import flashmlp_amd as fm
+from oracle import emulate, reference
 from oracle.inputs import make_inputs
 
 pytestmark = pytest.mark.gpu
@@ -66,3 +68,21 @@ def test_compiled_module_matches_eager():
     torch.cuda.synchronize()
     assert torch.equal(o_c, o_e)
     assert torch.equal(g_c[0], m.w1.grad) and torch.equal(g_c[1], m.w2.grad)
+
+
+@pytest.mark.parametrize("dt,act", [(torch.bfloat16, "silu"), (torch.float16, "sigmoid"), (torch.bfloat16, "leaky_relu")],
+                         ids=["bf16-silu", "f16-sigmoid", "bf16-leaky"])
+def test_compiled_op_matches_oracle(dt, act):
+    # O and dX elementwise against fp32 autograd; dW1, dW2 elementwise against the
+    # cast-point emulation and normwise (1e-2) against fp32, through the traced operator
+    _say(f"[ops] compiled operator vs oracle {dt} act='{act}'")
+    x, w1, w2, do = make_inputs(3, 333, 128, 264, dt, seed=13)
+    compiled = torch.compile(lambda a, b, c: fm.flashmlp(a, b, c, act), backend="aot_eager", fullgraph=True)
+    o, dx, dw1, dw2 = (t.float().cpu() for t in _loss_and_grads(compiled, *(t.cuda() for t in (x, w1, w2, do))))
+    ro, rdx, rdw1, rdw2 = reference.autograd_grads(x, w1, w2, do, act)
+    _, edw1, edw2 = emulate.emu_bwd(x, w1, w2, do, act, dt)
+    close = lambda a, b: bool(((a - b).abs() <= 3e-2 + 3e-2 * b.abs()).all())
+    rel = lambda a, b: ((a - b).norm() / b.norm()).item()
+    assert close(o, ro) and close(dx, rdx)
+    assert close(dw1, edw1) and close(dw2, edw2)
+    assert rel(dw1, rdw1) <= 1e-2 and rel(dw2, rdw2) <= 1e-2

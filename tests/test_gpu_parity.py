@@ -119,11 +119,25 @@ def test_reference_shapes():
     run_case("ref-autograd-shape", 8, 512, 64, 512, torch.bfloat16, "silu", seed=42)
 
 
+# Regression guard on dW against the fp32 oracle at the bf16 configurations: rounding h and
+# dZ to bf16 (the reference's cast points) leaves this share of dW elements just outside the
+# elementwise 3e-2 bar (CPU emulation of the same cast points: cfg3 1.57 % / 2.28 %, cfg4
+# 1.48 % / 2.61 %). A kernel change that stays within the normwise 1e-2 but loses accuracy
+# elementwise shows up here.
+DW_FP32_MISS_BOUND = {"cfg3": (0.019, 0.028), "cfg4": (0.018, 0.031)}
+
+
 @pytest.mark.parametrize("name", ["cfg2", "cfg3", "cfg5_linear", "cfg5_sigmoid"])
 def test_config(name):
     c = CONFIGS[name]
     heads = None if c.H * c.B <= 16 * 4097 else [0, c.H - 1]
-    run_case(name, c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=heads)
+    res = run_case(name, c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=heads)
+    if name in DW_FP32_MISS_BOUND:
+        b1, b2 = DW_FP32_MISS_BOUND[name]
+        assert res["dw1_fail_vs_fp32"] <= b1 and res["dw2_fail_vs_fp32"] <= b2, res
+    elif c.dtype == torch.float16:
+        # fp16 keeps 3 more bits of h and dZ: dW passes the bar against fp32 itself
+        assert res["dw1_fail_vs_fp32"] <= 1e-3 and res["dw2_fail_vs_fp32"] <= 1e-3, res
 
 
 def test_config4_north_star():
@@ -131,3 +145,13 @@ def test_config4_north_star():
     res = run_case("cfg4", c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=[0, 17, 31])
     _say(f"[parity] cfg4 dW elementwise-3e-2 fraction vs fp32 oracle: dW1 {res['dw1_fail_vs_fp32']:.4f} "
          f"dW2 {res['dw2_fail_vs_fp32']:.4f}")
+    b1, b2 = DW_FP32_MISS_BOUND["cfg4"]
+    assert res["dw1_fail_vs_fp32"] <= b1 and res["dw2_fail_vs_fp32"] <= b2, res
+
+
+@pytest.mark.parametrize("act", ["", "sigmoid"], ids=["linear", "sigmoid"])
+def test_config5s_forward_sweep(act):
+    # the fp16 forward-only inference sweep at B = 65536
+    # (H=8 D=64 E=2048, X ~ N(0, 4)); heads 0 and 7 against the oracle (heads are independent)
+    c = CONFIGS["cfg5s"]
+    run_case("cfg5s", c.H, c.B, c.D, c.E, c.dtype, act, c.x_std, heads=[0, c.H - 1], check_bwd=False)

@@ -173,3 +173,102 @@ def test_inputs_seeded_and_scaled():
     assert abs(w1.std().item() - 128 ** -0.5) < 0.005
     assert abs(w2.std().item() - 512 ** -0.5) < 0.002
     assert abs(do.std().item() - 1.0) < 0.02
+
+
+# ---- emu_bwd's cast points, pinned against the blockwise restatement of the reference's
+# backward programs (oracle/blockwise.py follows flashmlp.py:165-329 tile by tile) ----
+
+def _rel(a, b):
+    return ((a.double() - b.double()).norm() / b.double().norm()).item()
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("act", ACTS)
+def test_emu_bwd_matches_blockwise_programs(act, dt):
+    # same cast points, different tiling and summation order: only fp32 rounding noise
+    from oracle import blockwise
+
+    x, w1, w2, do = make_inputs(2, 256, 64, 256, dt, seed=11)
+    e = emulate.emu_bwd(x, w1, w2, do, act, dt, round_out=False)
+    b = blockwise.bwd_blocks(x, w1, w2, do, act, dt, deriv="fp32", round_out=False)
+    for u, v in zip(e, b):
+        assert _rel(u, v) < 2e-5
+    # rounded outputs: a summation-order difference can flip an output's last io bit
+    ulp = 2.0 ** -7 if dt == torch.bfloat16 else 2.0 ** -10
+    e = emulate.emu_bwd(x, w1, w2, do, act, dt)
+    b = blockwise.bwd_blocks(x, w1, w2, do, act, dt, deriv="fp32")
+    for u, v in zip(e, b):
+        diff = (u - v).abs()
+        assert (diff > 0).float().mean().item() < 0.01
+        # small outputs are sums with cancellation, where fp32 order noise can reach two io ulps
+        rms = v.pow(2).mean().sqrt()
+        assert (diff <= 2 * ulp * v.abs() + 1e-4 * rms).all()
+
+
+def _planted(x, w1, w2, do, act, dt, variant):
+    """emu_bwd with one cast point planted wrong (each is a plausible emulation mistake)."""
+    xs, a, b, g = (t.float() for t in (x, w1, w2, do))
+    z = torch.bmm(xs, a)
+    dh = torch.bmm(g, b.transpose(1, 2))
+    q = lambda t: t.to(dt).float()
+    h = emulate._h(z, act)
+    dz = emulate._dz(z, dh, act)
+    if variant == "no_h_cast":
+        dz = q(dz)
+    elif variant == "no_dz_cast":
+        h = q(h)
+    elif variant == "dh_cast_not_dz":
+        h, dz = q(h), emulate._dz(z, q(dh), act)
+    return torch.bmm(dz, a.transpose(1, 2)), torch.bmm(xs.transpose(1, 2), dz), torch.bmm(h.transpose(1, 2), g)
+
+
+@pytest.mark.parametrize("act", ["silu", "sigmoid"])
+@pytest.mark.parametrize("variant,moved", [("no_h_cast", (2,)), ("no_dz_cast", (0, 1)), ("dh_cast_not_dz", (0, 1))])
+def test_planted_bwd_cast_mistakes_are_detected(act, variant, moved):
+    # each planted variant moves the outputs its cast feeds by far more than the 1e-4 bar of
+    # the fp32-sum tests, while emu_bwd stays within fp32 noise of the blockwise programs
+    from oracle import blockwise
+
+    dt = torch.bfloat16
+    x, w1, w2, do = make_inputs(2, 256, 64, 256, dt, seed=12)
+    ref = blockwise.bwd_blocks(x, w1, w2, do, act, dt, deriv="fp32", round_out=False)
+    good = emulate.emu_bwd(x, w1, w2, do, act, dt, round_out=False)
+    bad = _planted(x, w1, w2, do, act, dt, variant)
+    for i in range(3):
+        assert _rel(good[i], ref[i]) < 2e-5
+        if i in moved:
+            assert _rel(bad[i], ref[i]) > 5e-4, (variant, i)
+        else:
+            assert _rel(bad[i], ref[i]) < 2e-5, (variant, i)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("act", ["silu", "sigmoid"])
+def test_fp32_derivative_is_closer_to_autograd_than_rounded_h(act, dt):
+    # the kernels (and emu_bwd) evaluate SiLU's and sigmoid's derivative from the fp32
+    # sigmoid; the reference kernel uses the io-rounded h (flashmlp.py:230-233, :315-318).
+    # Both round dZ to the io dtype; against the fp32 autograd oracle the fp32 form is the
+    # closer of the two, and they differ by ~1e-3 (bf16) normwise in dX and dW1.
+    from oracle import blockwise
+
+    x, w1, w2, do = make_inputs(2, 256, 64, 256, dt, seed=11)
+    _, rdx, rdw1, rdw2 = reference.autograd_grads(x, w1, w2, do, act)
+    f = blockwise.bwd_blocks(x, w1, w2, do, act, dt, deriv="fp32", round_out=False)
+    r = blockwise.bwd_blocks(x, w1, w2, do, act, dt, deriv="reference", round_out=False)
+    assert _rel(f[0], rdx) < _rel(r[0], rdx)
+    assert _rel(f[1], rdw1) < _rel(r[1], rdw1)
+    assert torch.equal(f[2], r[2])  # dW2 does not involve the derivative
+
+
+def test_blockwise_reference_derivative_leaky_kink():
+    # literal reference derivative: slope 1 at z == 0 (flashmlp.py:33-34); the fp32 form
+    # follows autograd (0.01). Zero X rows make every z == 0.
+    from oracle import blockwise
+
+    x = torch.zeros(1, 4, 16)
+    w1 = torch.randn(1, 16, 8)
+    w2 = torch.randn(1, 8, 16)
+    do = torch.randn(1, 4, 16)
+    r = blockwise.bwd_blocks(x, w1, w2, do, "leaky_relu", torch.float32, deriv="reference", round_out=False)
+    f = blockwise.bwd_blocks(x, w1, w2, do, "leaky_relu", torch.float32, deriv="fp32", round_out=False)
+    torch.testing.assert_close(r[0], f[0] * 100)
