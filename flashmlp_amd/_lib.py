@@ -31,7 +31,10 @@ SIGNATURES = {
     "fmlp_bwd_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, ctypes.c_int]),
     "fmlp_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int,
                                 ctypes.c_int, _vp, ctypes.c_size_t, _vp]),
+    "fmlp_bwd_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int,
+                                        ctypes.c_int, _vp]),
 }
+FMLP_SCRATCH_MAX_BYTES = 64 << 20
 
 _lock = threading.Lock()
 _lib = None

@@ -13,6 +13,8 @@
 
 #define FMLP_EXPORT extern "C" __attribute__((visibility("default")))
 
+static_assert(fmlp::kScratchBytes == FMLP_SCRATCH_MAX_BYTES, "scratch size in the header and the library");
+
 int fmlp::env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
   if (v == nullptr || *v == 0) return dflt;
@@ -164,9 +166,13 @@ FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int
   return fmlp::plan_bwd(H, B, D, E, cus).ws_bytes;
 }
 
-FMLP_EXPORT int fmlp_bwd(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1,
-                         void* dw2, int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, void* workspace,
-                         size_t workspace_bytes, void* stream) {
+namespace {
+
+// Argument checks shared by fmlp_bwd and fmlp_bwd_noalloc; fills the plan when there is
+// work (returns FMLP_OK with *work = false for H == 0).
+int bwd_prepare(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1, void* dw2,
+                int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, fmlp::BwdPlan* plan, bool* work) {
+  *work = false;
   int st = check_shape(H, B, D, E, dtype);
   if (st) return st;
   if ((st = check_act(act))) return st;
@@ -176,16 +182,55 @@ FMLP_EXPORT int fmlp_bwd(const void* x, const void* w1, const void* w2, const vo
       (st = check_ptr(dout, "dout", rows)) || (st = check_ptr(dx, "dx", rows)) || (st = check_ptr(dw1, "dw1", wts)) ||
       (st = check_ptr(dw2, "dw2", wts)))
     return st;
-  if (H == 0) return ok();
+  if (H == 0) return FMLP_OK;
   int cus = 0;
   if ((st = num_cus_current(&cus))) return st;
-  const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, cus);
+  *plan = fmlp::plan_bwd(H, B, D, E, cus);
+  *work = true;
+  return FMLP_OK;
+}
+
+}  // namespace
+
+FMLP_EXPORT int fmlp_bwd(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1,
+                         void* dw2, int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, void* workspace,
+                         size_t workspace_bytes, void* stream) {
+  fmlp::BwdPlan plan{};
+  bool work = false;
+  int st = bwd_prepare(x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, dtype, act, &plan, &work);
+  if (st) return st;
+  if (!work) return ok();
   if (plan.ws_bytes > 0) {
     if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
       return fail(FMLP_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, plan.ws_bytes);
     if (!aligned16(workspace)) return fail(FMLP_ERR_INVALID_ARG, "workspace is not 16-byte aligned");
   }
   fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, (dtype & ~FMLP_OUT_F32) == FMLP_DTYPE_BF16, act, workspace,
+                  (dtype & FMLP_OUT_F32) != 0};
+  hipError_t e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  return ok();
+}
+
+FMLP_EXPORT int fmlp_bwd_noalloc(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1,
+                                 void* dw2, int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act,
+                                 void* stream) {
+  fmlp::BwdPlan plan{};
+  bool work = false;
+  int st = bwd_prepare(x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, dtype, act, &plan, &work);
+  if (st) return st;
+  if (!work) return ok();
+  void* scratch = nullptr;
+  if (plan.ws_bytes > 0) {
+    if (plan.ws_bytes > fmlp::kScratchBytes)
+      return fail(FMLP_ERR_WORKSPACE,
+                  "fmlp_bwd_noalloc: these shapes need %zu bytes of scratch, the static scratch holds %zu "
+                  "(FMLP_SCRATCH_MAX_BYTES); call fmlp_bwd with a workspace instead",
+                  plan.ws_bytes, fmlp::kScratchBytes);
+    hipError_t e = fmlp::scratch_current_device(&scratch);
+    if (e != hipSuccess) return fail(FMLP_ERR_HIP, "scratch lookup: %s", hipGetErrorString(e));
+  }
+  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, (dtype & ~FMLP_OUT_F32) == FMLP_DTYPE_BF16, act, scratch,
                   (dtype & FMLP_OUT_F32) != 0};
   hipError_t e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));

@@ -62,4 +62,9 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus);
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t st);
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st);
 
+// The library's static device scratch (fmlp_bwd_noalloc): its device address on the current
+// device, looked up once per device, and its size in bytes.
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+hipError_t scratch_current_device(void** ptr);
+
 }  // namespace fmlp

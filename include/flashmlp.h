@@ -87,6 +87,20 @@ int fmlp_bwd(const void* x, const void* w1, const void* w2, const void* dout, vo
              int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, void* workspace,
              size_t workspace_bytes, void* stream);
 
+/*
+ * Backward without allocation: fmlp_bwd with the workspace replaced by the library's own
+ * static device scratch (FMLP_SCRATCH_MAX_BYTES per device, held from the first call on a
+ * device until the process ends). No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). It calls no hipMalloc, hipFree or allocating routine. Shapes whose
+ * fmlp_bwd_workspace_bytes() exceeds FMLP_SCRATCH_MAX_BYTES return FMLP_ERR_WORKSPACE. All
+ * calls on one device share that device's scratch: calls that overlap on one device (other
+ * streams, other threads) race; serialise them.
+ */
+#define FMLP_SCRATCH_MAX_BYTES ((size_t)64 << 20)
+int fmlp_bwd_noalloc(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1, void* dw2,
+                     int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,98 @@
+"""fmlp_bwd_noalloc (the backward with the library's static device scratch in place of a
+caller workspace) against fmlp_bwd with a torch-allocated workspace, through the C ABI.
+
+Two calls in a row on shapes whose dW programs split B (so the scratch holds the fp32
+partials), the second with a smaller input: the second call must not see the first call's
+partials. Results are compared elementwise at the parity bar (atol = rtol = 3e-2) and
+must in fact be bit-identical (same kernels, same plan, same summation order). On a 256-CU
+MI355X the partials of every supported shape fit FMLP_SCRATCH_MAX_BYTES.
+"""
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from flashmlp_amd import _lib
+from oracle.inputs import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+_DT = {torch.float16: _lib.FMLP_DTYPE_F16, torch.bfloat16: _lib.FMLP_DTYPE_BF16}
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _outs(x, w1):
+    H, B, D = x.shape
+    E = w1.shape[2]
+    return (torch.empty_like(x), torch.empty(H, D, E, dtype=x.dtype, device=x.device),
+            torch.empty(H, E, D, dtype=x.dtype, device=x.device))
+
+
+def _bwd_ws(L, x, w1, w2, do, act):
+    H, B, D = x.shape
+    E = w1.shape[2]
+    code = _DT[x.dtype]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    n = L.fmlp_bwd_workspace_bytes(H, B, D, E, code)
+    ws = torch.empty(max(n, 16), dtype=torch.uint8, device=x.device)
+    dx, dw1, dw2 = _outs(x, w1)
+    _lib.check(L.fmlp_bwd(_p(x), _p(w1), _p(w2), _p(do), _p(dx), _p(dw1), _p(dw2), H, B, D, E, code,
+                          _lib.ACT_CODES[act], _p(ws), n, stream), "backward")
+    return (dx, dw1, dw2), n
+
+
+def _bwd_noalloc(L, x, w1, w2, do, act):
+    H, B, D = x.shape
+    E = w1.shape[2]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dx, dw1, dw2 = _outs(x, w1)
+    _lib.check(L.fmlp_bwd_noalloc(_p(x), _p(w1), _p(w2), _p(do), _p(dx), _p(dw1), _p(dw2), H, B, D, E,
+                                  _DT[x.dtype], _lib.ACT_CODES[act], stream), "backward (no allocation)")
+    return dx, dw1, dw2
+
+
+def test_noalloc_matches_workspace_entry_point_twice():
+    L = _lib.lib()
+    # first: the cfg3 shape (B split 4 ways, 33.5 MB of partials); second: smaller
+    cases = [(16, 8192, 128, 512, torch.bfloat16, "leaky_relu", 21), (6, 1500, 64, 264, torch.float16, "silu", 22)]
+    for H, B, D, E, dt, act, seed in cases:
+        _say(f"[noalloc] H={H} B={B} D={D} E={E} {dt} act='{act}' seed={seed}")
+        x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=seed))
+        ref, n = _bwd_ws(L, x, w1, w2, do, act)
+        assert 0 < n <= _lib.FMLP_SCRATCH_MAX_BYTES, n  # the scratch path is exercised
+        got = _bwd_noalloc(L, x, w1, w2, do, act)
+        torch.cuda.synchronize()
+        for g, r in zip(got, ref):
+            g, r = g.float(), r.float()
+            assert bool(((g - r).abs() <= 3e-2 + 3e-2 * r.abs()).all())
+            assert torch.equal(g, r)
+        _say(f"[noalloc] H={H} B={B}: identical to fmlp_bwd (workspace {n} bytes)")
+
+
+def test_noalloc_without_split_and_scratch_bound():
+    L = _lib.lib()
+    # the cfg4 head count and E: 256 dW programs, one B split, no scratch needed
+    H, B, D, E = 32, 600, 128, 1024
+    x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, torch.bfloat16, seed=23))
+    _say(f"[noalloc] no-split H={H} B={B} D={D} E={E}")
+    ref, n = _bwd_ws(L, x, w1, w2, do, "silu")
+    got = _bwd_noalloc(L, x, w1, w2, do, "silu")
+    torch.cuda.synchronize()
+    assert n == 0
+    for g, r in zip(got, ref):
+        assert torch.equal(g, r)
+    # the fp32 partials exist only while H * ceil(E / 128) dW programs leave CUs idle; their
+    # size peaks just below one program per CU: at D = 128 every supported shape fits
+    worst = max(L.fmlp_bwd_workspace_bytes(h, 1 << 20, 128, 128 * ne, _lib.FMLP_DTYPE_BF16)
+                for h in range(1, 300) for ne in (1, 2, 3))
+    _say(f"[noalloc] largest partial workspace over H <= 299, E <= 384, D = 128: {worst} bytes")
+    assert 0 < worst <= _lib.FMLP_SCRATCH_MAX_BYTES
