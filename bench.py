@@ -18,7 +18,9 @@ the same workload, plus the reference's CPU configuration (cfg1) in full.
 
 Other workloads: cfg2, cfg3, cfg5, cfg5_linear (fwd+bwd), cfg5s
 (forward-only, reports HBM GB/s), example (the four shapes of the reference's
-performance.md through the FlashMLP module, timed as example.py times them).
+performance.md through the FlashMLP module, timed as example.py times them), mfma_ceiling
+(the sustained bf16 MFMA rate of the device: register-fed v_mfma_f32_32x32x16_bf16 chains, two
+waves per SIMD, random and all-zero operands; libfmlp_ceiling.so).
 """
 from __future__ import annotations
 
@@ -281,12 +283,45 @@ def run_example(args):
     print(json.dumps(line), flush=True)
 
 
+def run_mfma_ceiling(args):
+    """Sustained executed bf16 MFMA rate with operands in registers (no memory traffic), random
+    and all-zero operand bits: the power-limited ceiling the FlashMLP kernels are compared with."""
+    import ctypes
+
+    import torch
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "flashmlp_amd", "libfmlp_ceiling.so"))
+    lib.fmlp_ceiling_mfma.restype = ctypes.c_int
+    ncu = torch.cuda.get_device_properties(0).multi_processor_count
+    grid, iters = 2 * ncu, 4000  # two waves per SIMD
+    out = torch.empty(grid * 256, device="cuda", dtype=torch.float32)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    flops = float(grid) * 4 * iters * 4 * 32768
+    res = {}
+    for name, zero in (("random", 0), ("zero", 1)):
+        def call():
+            r = lib.fmlp_ceiling_mfma(ctypes.c_void_p(out.data_ptr()), iters, zero, grid, st)
+            if r != 0:
+                raise RuntimeError(f"fmlp_ceiling_mfma: hip error {r}")
+        for _ in range(args.warmup + 20):
+            call()
+        torch.cuda.synchronize()
+        ms = _wall_ms(call, max(args.steps, 50))
+        res[name] = {"tflops": round(flops / (ms * 1e-3) / 1e12, 1), "ms_per_launch": round(ms, 4)}
+    peak = PEAK_TFLOPS["bf16"]
+    line = {"metric": "sustained bf16 MFMA rate (v_mfma_f32_32x32x16_bf16, register operands)", "workload": "mfma_ceiling",
+            "unit": "TFLOP/s", "peak": peak, "random": res["random"], "zero": res["zero"],
+            "random_frac_of_peak": round(res["random"]["tflops"] / peak, 4),
+            "config": {"grid": grid, "waves_per_simd": 2, "mfma_per_wave": iters * 4, "chains_per_wave": 4}}
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="cfg4", choices=sorted(WORKLOADS) + ["example"])
+    ap.add_argument("--workload", default="cfg4", choices=sorted(WORKLOADS) + ["example", "mfma_ceiling"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-memory", action="store_true", help="skip the peak-memory comparison")
     ap.add_argument("--no-extra", action="store_true", help="skip the autograd-step and host-overhead timings")
@@ -308,6 +343,9 @@ def main():
     torch.cuda.set_device(0)
     if args.workload == "example":
         run_example(args)
+        return
+    if args.workload == "mfma_ceiling":
+        run_mfma_ceiling(args)
         return
 
     H, B, D, E, dt_name, act, x_std, fwd_only = WORKLOADS[args.workload]

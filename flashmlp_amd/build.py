@@ -3,7 +3,9 @@
     python -m flashmlp_amd.build          # writes flashmlp_amd/libflashmlp.so
 
 The library is a plain shared object: host code calls it through include/flashmlp.h
-(ctypes from Python). Cross-compiles on a machine without a GPU.
+(ctypes from Python). Cross-compiles on a machine without a GPU. The MFMA-ceiling
+measurement kernel (fmlp_ceiling.hip, used by bench.py only) goes into its own
+libfmlp_ceiling.so.
 """
 from __future__ import annotations
 
@@ -20,6 +22,8 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libflashmlp.so"
 SOURCES = ["fmlp_fwd.hip", "fmlp_bwd.hip", "fmlp_abi.cpp"]
+CEILING_SRC = "fmlp_ceiling.hip"
+CEILING_LIB = PKG / "libfmlp_ceiling.so"
 ARCH = os.environ.get("FLASHMLP_ARCH", "gfx950")
 
 # Packed fp32 VALU forms are disabled for every device pass.
@@ -50,19 +54,26 @@ def _compile(src: str, verbose: bool) -> Path:
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compile every source and link flashmlp_amd/libflashmlp.so. Always rebuilds."""
-    BUILD.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=len(SOURCES)) as ex:
-        objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
-    tmp = LIB.with_suffix(".so.tmp")
+def _link(objs, lib: Path, verbose: bool) -> None:
+    tmp = lib.with_suffix(".so.tmp")
     cmd = [_hipcc(), "-shared", "-fPIC", f"--offload-arch={ARCH}", *[str(o) for o in objs], "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}{res.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose: bool = False) -> Path:
+    """Compile every source and link flashmlp_amd/libflashmlp.so (and the measurement-only
+    libfmlp_ceiling.so). Always rebuilds."""
+    BUILD.mkdir(exist_ok=True)
+    srcs = SOURCES + [CEILING_SRC]
+    with ThreadPoolExecutor(max_workers=len(srcs)) as ex:
+        objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
+    _link(objs[:len(SOURCES)], LIB, verbose)
+    _link(objs[len(SOURCES):], CEILING_LIB, verbose)
     return LIB
 
 

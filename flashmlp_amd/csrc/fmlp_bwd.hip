@@ -396,9 +396,10 @@ constexpr int DX2_NT = DX2_NW * 64;
 constexpr int DX2_ROWS = DX2_NW * 32;
 
 template <bool BF16, int D, int ACT>
-__global__ void __launch_bounds__(DX2_NT)
-dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-           const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
+__device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* __restrict__ W1,
+                                         const u16* __restrict__ W2, const u16* __restrict__ dO,
+                                         void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32,
+                                         int t) {
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr unsigned SLOT = 128u * D;
   constexpr unsigned W2OFF = 64u * D;
@@ -409,7 +410,7 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
-  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  
   const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
   const int NC = (E + 31) >> 5;
   const bool late = wave >= 4;  // VALU-first half of the workgroup
@@ -621,10 +622,11 @@ __device__ __forceinline__ unsigned wt_off(unsigned r, unsigned q) {
 }
 
 template <bool BF16, int D, int ACT>
-__global__ void __launch_bounds__(DW2_NT)
-dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-           const u16* __restrict__ dO, void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
-           int H, int B, int E, int nE, int nS, int rows_per_split, int outf32) {
+__device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* __restrict__ W1,
+                                         const u16* __restrict__ W2, const u16* __restrict__ dO,
+                                         void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
+                                         int H, int B, int E, int nE, int nS, int rows_per_split, int outf32,
+                                         int t) {
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr int SUB = 64 * D;            // bytes of a [32][D] subtile
   constexpr int PAIR = 4 * SUB;          // X set0, dO set0, X set1, dO set1
@@ -641,7 +643,6 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
   const int cg = wave & 3, set = wave >> 2;
-  const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int et = t % nE;
   const int hs = t / nE;
   const int s = hs % nS, h = hs / nS;
@@ -872,6 +873,43 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 
 // dX programs: 4 waves; at D = 64 two workgroups share a CU (two waves per SIMD), at
 // D = 128 the role needs more than 256 VGPRs and runs one wave per SIMD.
+template <bool BF16, int D, int ACT>
+__global__ void __launch_bounds__(DX2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+           const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
+  dx2_body<BF16, D, ACT>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32, xcd_remap(blockIdx.x, gridDim.x));
+}
+
+template <bool BF16, int D, int ACT>
+__global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+           const u16* __restrict__ dO, void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
+           int H, int B, int E, int nE, int nS, int rows_per_split, int outf32) {
+  dw2_body<BF16, D, ACT>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32,
+                         xcd_remap(blockIdx.x, gridDim.x));
+}
+
+// Unified backward launch (flashmlp.py:341-421's program-id split): workgroups
+// [0, n_dw) are dW programs, the rest dX programs, so dX programs start on the CUs that
+// finish their dW programs first. Both roles use 8 waves (two per SIMD); the dynamic LDS
+// is the dW role's (the larger). Each role's tiles are remapped onto XCDs within its own
+// range (exact when n_dw is a multiple of 8).
+static_assert(DW2_NT == DX2_NT, "both roles run with the same workgroup size");
+template <bool BF16, int D, int ACT>
+__global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+           const u16* __restrict__ dO, void* __restrict__ dX, void* __restrict__ dW1, void* __restrict__ dW2,
+           float* __restrict__ ws, int H, int B, int E, int nE, int nS, int rows_per_split, int n_dw,
+           int dx_tiles_per_head, int outf32) {
+  const int b = blockIdx.x;
+  if (b < n_dw) {
+    dw2_body<BF16, D, ACT>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32, xcd_remap(b, n_dw));
+  } else {
+    dx2_body<BF16, D, ACT>(X, W1, W2, dO, dX, B, E, dx_tiles_per_head, outf32,
+                           xcd_remap(b - n_dw, (int)gridDim.x - n_dw));
+  }
+}
+
 template <bool BF16, int D, int ACT, int MT>
 __global__ void __launch_bounds__(DX_WAVES * 64)
 dx_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
@@ -943,6 +981,31 @@ template <bool BF16, int D, int ACT>
 static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
   if (p.n_dw > 0x7fffffffLL || p.n_dx > 0x7fffffffLL) return hipErrorInvalidValue;
   hipError_t e;
+  // FMLP_BWD_UNIFIED (read once per process): 1 (default) = one launch holding both roles
+  // when the dX programs use the 8-wave form, 0 = dW and dX programs as two launches
+  static const int unified = env_int("FMLP_BWD_UNIFIED", 1);
+  if (unified && p.dx_kind == 1 && p.n_dw > 0 && p.n_dx > 0) {
+    if (p.n_dw + p.n_dx > 0x7fffffffLL) return hipErrorInvalidValue;
+    const size_t lds = 1280u * D;  // the dW role's LDS (the dX role uses the first 512 D bytes)
+    auto k = bwd_kernel<BF16, D, ACT>;
+    static std::atomic<unsigned long long> lds_set{0};
+    e = set_lds_once((const void*)k, (int)lds, lds_set);
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, dim3((unsigned)(p.n_dw + p.n_dx)), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                       (const u16*)a.w2, (const u16*)a.dout, a.dx, a.dw1, a.dw2, (float*)a.ws, (int)a.H, (int)a.B,
+                       (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw, p.dx_tiles_per_head, a.out_f32 ? 1 : 0);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    if (p.nS > 1) {
+      const size_t per = (size_t)a.H * a.E * a.D;
+      size_t blocks = (per + 255) / 256;
+      if (blocks > 8192) blocks = 8192;
+      hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws,
+                         a.dw1, a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
+      e = hipGetLastError();
+    }
+    return e;
+  }
   // dW programs (and their partial reduction), then dX programs, in stream order
   if (p.n_dw > 0) {
     const size_t lds = 1280u * D;  // two weight tiles (256 D bytes each) + three subtile pairs (256 D each)

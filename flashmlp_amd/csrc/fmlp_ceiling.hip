@@ -1,0 +1,71 @@
+// Sustained bf16 MFMA ceiling of the device (measurement only, not part of the FlashMLP
+// path): every wave issues independent v_mfma_f32_32x32x16_bf16 chains with its operands
+// held in registers, two waves per SIMD, no memory traffic inside the loop. The rate it
+// reaches with random operand bits (versus all-zero operands) is the executed-MFMA rate the
+// part sustains at its power limit, the reference point for the kernels' MFMA busy figures.
+// Built into its own library (libfmlp_ceiling.so) and used by bench.py --workload mfma_ceiling.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kChains = 4;    // independent accumulators per wave
+constexpr int kThreads = 256;  // four waves per workgroup
+
+__device__ __forceinline__ unsigned mix(unsigned x) {
+  x ^= x >> 16;
+  x *= 0x7feb352du;
+  x ^= x >> 15;
+  x *= 0x846ca68bu;
+  x ^= x >> 16;
+  return x;
+}
+
+// bf16 with a random sign and mantissa and an exponent near 1 (finite for any chain length)
+__device__ __forceinline__ __bf16 rnd_bf16(unsigned h) {
+  const unsigned short bits = (unsigned short)((h & 0x807fu) | (0x3f00u + ((h >> 8) & 0x80u)));
+  return __builtin_bit_cast(__bf16, bits);
+}
+
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+mfma_ceiling_kernel(float* __restrict__ out, int iters, int zero_data) {
+  const unsigned gid = blockIdx.x * kThreads + threadIdx.x;
+  bf16x8 a[kChains], b[kChains];
+#pragma unroll
+  for (int c = 0; c < kChains; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const unsigned h = mix(gid * 64u + c * 8u + j);
+      a[c][j] = zero_data ? (__bf16)0.f : rnd_bf16(h);
+      b[c][j] = zero_data ? (__bf16)0.f : rnd_bf16(mix(h));
+    }
+  f32x16 acc[kChains];
+#pragma unroll
+  for (int c = 0; c < kChains; ++c)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[c][i] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int c = 0; c < kChains; ++c) acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[c], b[c], acc[c], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < kChains; ++c)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s += acc[c][i];
+  out[gid] = s;
+}
+
+}  // namespace
+
+// Launches `grid` workgroups of 256 threads, each wave issuing iters * 4 MFMAs; `out` holds
+// grid * 256 floats. Returns the hipError_t of the launch. FLOPs = grid * 4 * iters * 4 * 32768.
+extern "C" __attribute__((visibility("default"))) int fmlp_ceiling_mfma(void* out, int iters, int zero_data, int grid,
+                                                                        hipStream_t stream) {
+  if (out == nullptr || iters <= 0 || grid <= 0) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(mfma_ceiling_kernel, dim3((unsigned)grid), dim3(kThreads), 0, stream, (float*)out, iters, zero_data);
+  return (int)hipGetLastError();
+}

@@ -127,3 +127,15 @@ def test_last_error_is_thread_local(L):
     t.join()
     assert seen == [b""]
     assert b"D=96" in L.fmlp_last_error()
+
+
+def test_ceiling_library_exports_its_entry_point():
+    """The measurement-only MFMA-ceiling library (bench.py --workload mfma_ceiling) is built
+    beside libflashmlp.so and exports its one launcher."""
+    lib = ROOT / "flashmlp_amd" / "libfmlp_ceiling.so"
+    if not lib.exists():
+        pytest.skip("libfmlp_ceiling.so not built (python -m flashmlp_amd.build)")
+    out = subprocess.run(["nm", "-D", "--defined-only", str(lib)], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert "fmlp_ceiling_mfma" in exported
+    ctypes.CDLL(str(lib))  # loads without a GPU
