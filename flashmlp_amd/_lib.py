@@ -16,6 +16,8 @@ FMLP_DTYPE_F16 = 0
 FMLP_DTYPE_BF16 = 1
 # OR-ed into the dtype code: outputs are fp32 arrays holding the unrounded fp32 sums
 FMLP_OUT_F32 = 0x100
+# OR-ed into the backward's dtype code: dW products with hi/lo io-dtype terms of h and dZ
+FMLP_DW_HILO = 0x200
 ACT_CODES = {"": 0, "silu": 1, "leaky_relu": 2, "sigmoid": 3}
 
 # (name, restype, argtypes) for every symbol include/flashmlp.h declares

@@ -75,13 +75,17 @@ int num_cus_current(int* out) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// io dtype of a dtype argument (its flag bits removed)
+int io_of(int dtype) { return dtype & ~(FMLP_OUT_F32 | FMLP_DW_HILO); }
+
 int check_shape(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   if (H < 0 || B < 0 || D < 0 || E < 0)
     return fail(FMLP_ERR_INVALID_ARG, "negative dimension (H=%lld B=%lld D=%lld E=%lld)", (long long)H,
                 (long long)B, (long long)D, (long long)E);
-  const int io = dtype & ~FMLP_OUT_F32;
+  const int io = dtype & ~(FMLP_OUT_F32 | FMLP_DW_HILO);
   if (io != FMLP_DTYPE_F16 && io != FMLP_DTYPE_BF16)
-    return fail(FMLP_ERR_UNSUPPORTED, "dtype code %d: only fp16 (0) and bf16 (1) are supported, optionally with FMLP_OUT_F32",
+    return fail(FMLP_ERR_UNSUPPORTED,
+                "dtype code %d: only fp16 (0) and bf16 (1) are supported, optionally with FMLP_OUT_F32 / FMLP_DW_HILO",
                 dtype);
   if (D != 64 && D != 128) return fail(FMLP_ERR_UNSUPPORTED, "hidden dimension D=%lld: supported D are 64 and 128", (long long)D);
   if (E < 8 || E % 8 != 0)
@@ -144,6 +148,7 @@ FMLP_EXPORT int fmlp_shape_supported(int64_t H, int64_t B, int64_t D, int64_t E,
 
 FMLP_EXPORT int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
                          int64_t E, int dtype, int act, void* stream) {
+  if (dtype & FMLP_DW_HILO) return fail(FMLP_ERR_INVALID_ARG, "FMLP_DW_HILO applies to the backward only");
   int st = check_shape(H, B, D, E, dtype);
   if (st) return st;
   if ((st = check_act(act))) return st;
@@ -153,7 +158,7 @@ FMLP_EXPORT int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o,
       (st = check_ptr(o, "o", rows)))
     return st;
   if (!rows) return ok();
-  fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, (dtype & ~FMLP_OUT_F32) == FMLP_DTYPE_BF16, act, (dtype & FMLP_OUT_F32) != 0};
+  fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, io_of(dtype) == FMLP_DTYPE_BF16, act, (dtype & FMLP_OUT_F32) != 0};
   hipError_t e = fmlp::launch_fwd(a, (hipStream_t)stream);
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
   return ok();
@@ -205,8 +210,8 @@ FMLP_EXPORT int fmlp_bwd(const void* x, const void* w1, const void* w2, const vo
       return fail(FMLP_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, plan.ws_bytes);
     if (!aligned16(workspace)) return fail(FMLP_ERR_INVALID_ARG, "workspace is not 16-byte aligned");
   }
-  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, (dtype & ~FMLP_OUT_F32) == FMLP_DTYPE_BF16, act, workspace,
-                  (dtype & FMLP_OUT_F32) != 0};
+  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io_of(dtype) == FMLP_DTYPE_BF16, act, workspace,
+                  (dtype & FMLP_OUT_F32) != 0, (dtype & FMLP_DW_HILO) != 0};
   hipError_t e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return ok();
@@ -230,8 +235,8 @@ FMLP_EXPORT int fmlp_bwd_noalloc(const void* x, const void* w1, const void* w2, 
     hipError_t e = fmlp::scratch_current_device(&scratch);
     if (e != hipSuccess) return fail(FMLP_ERR_HIP, "scratch lookup: %s", hipGetErrorString(e));
   }
-  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, (dtype & ~FMLP_OUT_F32) == FMLP_DTYPE_BF16, act, scratch,
-                  (dtype & FMLP_OUT_F32) != 0};
+  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io_of(dtype) == FMLP_DTYPE_BF16, act, scratch,
+                  (dtype & FMLP_OUT_F32) != 0, (dtype & FMLP_DW_HILO) != 0};
   hipError_t e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return ok();

@@ -621,7 +621,11 @@ __device__ __forceinline__ unsigned wt_off(unsigned r, unsigned q) {
   return (q >> 2) * 8192u + r * 64u + (((q & 3u) ^ ((r >> 2) & 3u)) << 4);
 }
 
-template <bool BF16, int D, int ACT>
+// HILO: the dW products take h and dZ as two io-dtype terms, hi = round(v) and
+// lo = round(v - hi), instead of round(v) alone (twice the dW MFMAs, same operand reads);
+// an accuracy mode with no counterpart in the reference, whose kernel rounds h and dZ to
+// the io dtype (flashmlp.py:297-320).
+template <bool BF16, int D, int ACT, bool HILO>
 __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* __restrict__ W1,
                                          const u16* __restrict__ W2, const u16* __restrict__ dO,
                                          void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
@@ -723,6 +727,7 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
   }
   f32x16 z = zero16(), dh = zero16();
   u32x4 hT[2], dzT[2];
+  u32x4 hL[2], dzL[2];  // lo terms (HILO only)
 
   struct Opnd {
     u32x4 a, b;
@@ -766,8 +771,13 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
     auto act_elem = [&](int e, float (&hv)[16], float (&dv)[16]) {
       act_fb<ACT>(z[e], dh[e], hv[e], dv[e]);
       if (e & 1) {
-        hT[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1], hv[e]);
-        dzT[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
+        const unsigned ph = pack2<BF16>(hv[e - 1], hv[e]), pd = pack2<BF16>(dv[e - 1], dv[e]);
+        hT[e >> 3][(e >> 1) & 3] = ph;
+        dzT[e >> 3][(e >> 1) & 3] = pd;
+        if constexpr (HILO) {  // v - round(v) is exact in fp32; its rounding is the lo term
+          hL[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1] - lo_f32<BF16>(ph), hv[e] - hi_f32<BF16>(ph));
+          dzL[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1] - lo_f32<BF16>(pd), dv[e] - hi_f32<BF16>(pd));
+        }
       }
     };
     float hv[16], dv[16];
@@ -782,8 +792,13 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
       const u32x4 cur_op = ring[q % (PD + 1)];
       if (q + PD < N2) ring[(q + PD) % (PD + 1)] = fetch(q + PD);
       const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1;
-      if ((q & 1) == 0) a2[nt] = mfma<BF16>(hT[s2], cur_op, a2[nt]);
-      else a1[nt] = mfma<BF16>(dzT[s2], cur_op, a1[nt]);
+      if ((q & 1) == 0) {
+        a2[nt] = mfma<BF16>(hT[s2], cur_op, a2[nt]);
+        if constexpr (HILO) a2[nt] = mfma<BF16>(hL[s2], cur_op, a2[nt]);
+      } else {
+        a1[nt] = mfma<BF16>(dzT[s2], cur_op, a1[nt]);
+        if constexpr (HILO) a1[nt] = mfma<BF16>(dzL[s2], cur_op, a1[nt]);
+      }
 #pragma unroll
       for (int e = 8 + sched_elem_begin(q, N2 / 2, 8); e < 8 + sched_elem_begin(q + 1, N2 / 2, 8); ++e)
         if (e < 16) act_elem(e, hv, dv);
@@ -880,12 +895,12 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   dx2_body<BF16, D, ACT>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32, xcd_remap(blockIdx.x, gridDim.x));
 }
 
-template <bool BF16, int D, int ACT>
+template <bool BF16, int D, int ACT, bool HILO>
 __global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
            int H, int B, int E, int nE, int nS, int rows_per_split, int outf32) {
-  dw2_body<BF16, D, ACT>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32,
+  dw2_body<BF16, D, ACT, HILO>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32,
                          xcd_remap(blockIdx.x, gridDim.x));
 }
 
@@ -895,7 +910,7 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 // is the dW role's (the larger). Each role's tiles are remapped onto XCDs within its own
 // range (exact when n_dw is a multiple of 8).
 static_assert(DW2_NT == DX2_NT, "both roles run with the same workgroup size");
-template <bool BF16, int D, int ACT>
+template <bool BF16, int D, int ACT, bool HILO>
 __global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dX, void* __restrict__ dW1, void* __restrict__ dW2,
@@ -903,7 +918,7 @@ bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
            int dx_tiles_per_head, int outf32) {
   const int b = blockIdx.x;
   if (b < n_dw) {
-    dw2_body<BF16, D, ACT>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32, xcd_remap(b, n_dw));
+    dw2_body<BF16, D, ACT, HILO>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32, xcd_remap(b, n_dw));
   } else {
     dx2_body<BF16, D, ACT>(X, W1, W2, dO, dX, B, E, dx_tiles_per_head, outf32,
                            xcd_remap(b - n_dw, (int)gridDim.x - n_dw));
@@ -987,14 +1002,17 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   if (unified && p.dx_kind == 1 && p.n_dw > 0 && p.n_dx > 0) {
     if (p.n_dw + p.n_dx > 0x7fffffffLL) return hipErrorInvalidValue;
     const size_t lds = 1280u * D;  // the dW role's LDS (the dX role uses the first 512 D bytes)
-    auto k = bwd_kernel<BF16, D, ACT>;
-    static std::atomic<unsigned long long> lds_set{0};
-    e = set_lds_once((const void*)k, (int)lds, lds_set);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3((unsigned)(p.n_dw + p.n_dx)), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                       (const u16*)a.w2, (const u16*)a.dout, a.dx, a.dw1, a.dw2, (float*)a.ws, (int)a.H, (int)a.B,
-                       (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw, p.dx_tiles_per_head, a.out_f32 ? 1 : 0);
-    e = hipGetLastError();
+    auto launch_u = [&](auto k) {
+      static std::atomic<unsigned long long> lds_set{0};
+      hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
+      if (r != hipSuccess) return r;
+      hipLaunchKernelGGL(k, dim3((unsigned)(p.n_dw + p.n_dx)), dim3(DW2_NT), lds, st, (const u16*)a.x,
+                         (const u16*)a.w1, (const u16*)a.w2, (const u16*)a.dout, a.dx, a.dw1, a.dw2, (float*)a.ws,
+                         (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw,
+                         p.dx_tiles_per_head, a.out_f32 ? 1 : 0);
+      return hipGetLastError();
+    };
+    e = a.dw_hilo ? launch_u(bwd_kernel<BF16, D, ACT, true>) : launch_u(bwd_kernel<BF16, D, ACT, false>);
     if (e != hipSuccess) return e;
     if (p.nS > 1) {
       const size_t per = (size_t)a.H * a.E * a.D;
@@ -1009,14 +1027,16 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   // dW programs (and their partial reduction), then dX programs, in stream order
   if (p.n_dw > 0) {
     const size_t lds = 1280u * D;  // two weight tiles (256 D bytes each) + three subtile pairs (256 D each)
-    auto k = dw2_kernel<BF16, D, ACT>;
-    static std::atomic<unsigned long long> lds_set{0};
-    e = set_lds_once((const void*)k, (int)lds, lds_set);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                       (const u16*)a.w2, (const u16*)a.dout, a.dw1, a.dw2, (float*)a.ws, (int)a.H,
-                       (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, a.out_f32 ? 1 : 0);
-    e = hipGetLastError();
+    auto launch_w = [&](auto k) {
+      static std::atomic<unsigned long long> lds_set{0};
+      hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
+      if (r != hipSuccess) return r;
+      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                         (const u16*)a.w2, (const u16*)a.dout, a.dw1, a.dw2, (float*)a.ws, (int)a.H,
+                         (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, a.out_f32 ? 1 : 0);
+      return hipGetLastError();
+    };
+    e = a.dw_hilo ? launch_w(dw2_kernel<BF16, D, ACT, true>) : launch_w(dw2_kernel<BF16, D, ACT, false>);
     if (e != hipSuccess) return e;
     if (p.nS > 1) {
       const size_t per = (size_t)a.H * a.E * a.D;

@@ -75,6 +75,18 @@ __device__ __forceinline__ float to_f32(u16 h) {
   }
 }
 
+// the two 16-bit values of a pack2 dword (low half = first argument), widened exactly
+template <bool BF16>
+__device__ __forceinline__ float lo_f32(unsigned v) {
+  if constexpr (BF16) return __uint_as_float(v << 16);
+  else return (float)__builtin_bit_cast(_Float16, (u16)(v & 0xffffu));
+}
+template <bool BF16>
+__device__ __forceinline__ float hi_f32(unsigned v) {
+  if constexpr (BF16) return __uint_as_float(v & 0xffff0000u);
+  else return (float)__builtin_bit_cast(_Float16, (u16)(v >> 16));
+}
+
 template <bool BF16>
 __device__ __forceinline__ u16 from_f32(float f) {
   return (u16)(pack2<BF16>(f, 0.f) & 0xffffu);

@@ -56,6 +56,7 @@ struct BwdArgs {
   int act;
   void* ws;
   bool out_f32;  // outputs as fp32 (FMLP_OUT_F32)
+  bool dw_hilo;  // dW products with hi/lo terms of h and dZ (FMLP_DW_HILO)
 };
 
 BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus);

@@ -9,6 +9,11 @@ Same names, arguments, shapes and assertion messages as the reference module
     FlashMLP(num_heads, hidden_dim, intermediate_dim, activation="silu",
              dtype=torch.float16, device="cuda")
 
+plus one opt-in the reference does not have: accurate_dw=True (flashmlp_bwd keyword,
+FlashMLPFunction's fifth argument, FlashMLP constructor argument) computes dW1 and dW2 with
+h and dZ split into two io-dtype terms (hi + lo) instead of rounded to the io dtype, for
+elementwise agreement with an fp32 computation at large B (twice the dW MFMA work).
+
 O = act(X W1) W2 per head with act in {"", "silu", "leaky_relu", "sigmoid"}; an unknown
 activation string means linear, as in the reference. Every call launches the HIP kernels
 of libflashmlp.so asynchronously on torch's current stream of the tensors' device; there
@@ -105,11 +110,12 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
 
 
 def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.Tensor,
-                 activation: str = "") -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                 activation: str = "", *, accurate_dw: bool = False) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """FlashMLP backward pass (reference: flashmlp.py:480-538).
 
     Recomputes Z = x @ w1 and h = act(Z) instead of reading stored activations.
-    Returns (dx, dw1, dw2) shaped like (x, w1, w2).
+    Returns (dx, dw1, dw2) shaped like (x, w1, w2). accurate_dw=True (no counterpart in the
+    reference) takes h and dZ into the dW products as hi + lo io-dtype terms.
     """
     assert x.shape[0] == w1.shape[0], "Number of heads must match"
     assert x.shape[0] == w2.shape[0], "Number of heads must match"
@@ -143,7 +149,8 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
         stream = torch.cuda.current_stream(x.device).cuda_stream
         st = L.fmlp_bwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(), dw1.data_ptr(),
-                        dw2.data_ptr(), H, B, D, E, dtype, _act_code(activation),
+                        dw2.data_ptr(), H, B, D, E, dtype | (_lib.FMLP_DW_HILO if accurate_dw else 0),
+                        _act_code(activation),
                         ws.data_ptr() if ws is not None else None, ws_bytes, stream)
     _lib.check(st, "backward")
     return dx.reshape(H, B, D), dw1.reshape(H, D, E), dw2.reshape(H, E, D)
@@ -153,17 +160,18 @@ class FlashMLPFunction(torch.autograd.Function):
     """Autograd binding (reference: flashmlp.py:545-557). Saves only (x, w1, w2)."""
 
     @staticmethod
-    def forward(ctx, x, w1, w2, activation=""):
+    def forward(ctx, x, w1, w2, activation="", accurate_dw=False):
         o = flashmlp_fwd(x, w1, w2, activation)
         ctx.save_for_backward(x, w1, w2)
         ctx.activation = activation
+        ctx.accurate_dw = bool(accurate_dw)
         return o
 
     @staticmethod
     def backward(ctx, do):
         x, w1, w2 = ctx.saved_tensors
-        dx, dw1, dw2 = flashmlp_bwd(x, w1, w2, do, ctx.activation)
-        return dx, dw1, dw2, None
+        dx, dw1, dw2 = flashmlp_bwd(x, w1, w2, do, ctx.activation, accurate_dw=ctx.accurate_dw)
+        return dx, dw1, dw2, None, None
 
 
 class FlashMLP(torch.nn.Module):
@@ -176,6 +184,8 @@ class FlashMLP(torch.nn.Module):
         activation: "silu", "leaky_relu", "sigmoid" or ""
         dtype: weight dtype (float16 or bfloat16)
         device: device of the weights
+        accurate_dw: dW products with hi + lo terms of h and dZ (no counterpart in the
+            reference; see flashmlp_bwd)
 
     Parameters w1 (H, D, E) ~ randn / sqrt(E) and w2 (H, E, D) ~ randn / sqrt(D), as in
     the reference (flashmlp.py:586-591). A 2-D input (B, D) is expanded to every head and
@@ -183,12 +193,13 @@ class FlashMLP(torch.nn.Module):
     """
 
     def __init__(self, num_heads: int, hidden_dim: int, intermediate_dim: int,
-                 activation: str = "silu", dtype=torch.float16, device="cuda"):
+                 activation: str = "silu", dtype=torch.float16, device="cuda", accurate_dw: bool = False):
         super().__init__()
         self.num_heads = num_heads
         self.hidden_dim = hidden_dim
         self.intermediate_dim = intermediate_dim
         self.activation = activation
+        self.accurate_dw = accurate_dw
 
         self.w1 = torch.nn.Parameter(
             torch.randn(num_heads, hidden_dim, intermediate_dim, dtype=dtype, device=device) / np.sqrt(intermediate_dim)
@@ -207,9 +218,9 @@ class FlashMLP(torch.nn.Module):
         if torch.compiler.is_compiling():
             # the registered operator (flashmlp_amd.ops) is what torch.compile traces through
             from .ops import flashmlp as _op
-            o = _op(x, self.w1, self.w2, self.activation)
+            o = _op(x, self.w1, self.w2, self.activation, self.accurate_dw)
         else:
-            o = FlashMLPFunction.apply(x, self.w1, self.w2, self.activation)
+            o = FlashMLPFunction.apply(x, self.w1, self.w2, self.activation, self.accurate_dw)
 
         if squeeze_output:
             o = o.mean(dim=0)

@@ -45,6 +45,15 @@ typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1 } fmlp_dtype;
  * against an fp32 emulation of the reference's algorithm at 1e-4 relative. */
 #define FMLP_OUT_F32 0x100
 
+/* OR-ed into the dtype argument of fmlp_bwd / fmlp_bwd_noalloc (rejected by fmlp_fwd): the
+ * dW products take h and dZ as two io-dtype terms, hi = round(v) and lo = round(v - hi),
+ * so dw1 and dw2 carry about twice the io dtype's mantissa bits of h and dZ (dx is
+ * unchanged). An accuracy mode with no counterpart in the reference, whose kernel rounds h
+ * and dZ to the io dtype before the dW products (flashmlp.py:297-320): for callers that
+ * need dW elementwise close to an fp32 computation at large B. It doubles the MFMA work of
+ * the dW programs (8u -> 12u executed FLOPs, u = H B D E). */
+#define FMLP_DW_HILO 0x200
+
 /* Activation codes; names as in the reference ("", "silu", "leaky_relu", "sigmoid"). */
 typedef enum { FMLP_ACT_NONE = 0, FMLP_ACT_SILU = 1, FMLP_ACT_LEAKY_RELU = 2, FMLP_ACT_SIGMOID = 3 } fmlp_act;
 

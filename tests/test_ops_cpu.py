@@ -10,9 +10,10 @@ import flashmlp_amd  # noqa: F401  (registers torch.ops.flashmlp_amd)
 
 def test_schemas():
     assert str(torch.ops.flashmlp_amd.fwd.default._schema) == (
-        'flashmlp_amd::fwd(Tensor x, Tensor w1, Tensor w2, str activation="") -> Tensor')
+        'flashmlp_amd::fwd(Tensor x, Tensor w1, Tensor w2, str activation="", bool accurate_dw=False) -> Tensor')
     assert str(torch.ops.flashmlp_amd.bwd.default._schema) == (
-        'flashmlp_amd::bwd(Tensor x, Tensor w1, Tensor w2, Tensor do, str activation="") -> (Tensor, Tensor, Tensor)')
+        'flashmlp_amd::bwd(Tensor x, Tensor w1, Tensor w2, Tensor do, str activation="", bool accurate_dw=False) '
+        '-> (Tensor, Tensor, Tensor)')
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
