@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().with_name("libflashmlp.so")
 FMLP_OK = 0
 FMLP_DTYPE_F16 = 0
 FMLP_DTYPE_BF16 = 1
+FMLP_DTYPE_F32 = 2
 # OR-ed into the dtype code: outputs are fp32 arrays holding the unrounded fp32 sums
 FMLP_OUT_F32 = 0x100
 # OR-ed into the backward's dtype code: dW products with hi/lo io-dtype terms of h and dZ
@@ -23,16 +24,22 @@ ACT_CODES = {"": 0, "silu": 1, "leaky_relu": 2, "sigmoid": 3}
 # (name, restype, argtypes) for every symbol include/flashmlp.h declares
 _i64 = ctypes.c_int64
 _vp = ctypes.c_void_p
+_i64p = ctypes.POINTER(ctypes.c_int64)
 SIGNATURES = {
     "fmlp_abi_version": (ctypes.c_int, []),
     "fmlp_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "fmlp_last_error": (ctypes.c_char_p, []),
     "fmlp_act_from_name": (ctypes.c_int, [ctypes.c_char_p]),
     "fmlp_shape_supported": (ctypes.c_int, [_i64, _i64, _i64, _i64, ctypes.c_int]),
+    "fmlp_shape_tuned": (ctypes.c_int, [_i64, _i64, ctypes.c_int]),
     "fmlp_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp]),
+    "fmlp_fwd_strided": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p,
+                                        ctypes.c_int, ctypes.c_int, _vp]),
     "fmlp_bwd_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, ctypes.c_int]),
     "fmlp_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int,
                                 ctypes.c_int, _vp, ctypes.c_size_t, _vp]),
+    "fmlp_bwd_strided": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p,
+                                        _i64p, _i64p, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_size_t, _vp]),
     "fmlp_bwd_noalloc": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int,
                                         ctypes.c_int, _vp]),
 }
@@ -64,6 +71,11 @@ def lib() -> ctypes.CDLL:
                 raise FlashMLPLibraryError("libflashmlp.so ABI version mismatch; rebuild it")
             _lib = handle
     return _lib
+
+
+def strides(t) -> "ctypes.Array":
+    """The three element strides of a 3-D tensor as an int64_t[3] for the *_strided calls."""
+    return (ctypes.c_int64 * 3)(*t.stride())
 
 
 def check(status: int, what: str) -> None:

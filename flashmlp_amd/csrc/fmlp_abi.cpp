@@ -77,27 +77,34 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // io dtype of a dtype argument (its flag bits removed)
 int io_of(int dtype) { return dtype & ~(FMLP_OUT_F32 | FMLP_DW_HILO); }
+size_t elem_bytes(int io) { return io == FMLP_DTYPE_F32 ? 4 : 2; }
+
+// The tuned kernels (fmlp_fwd.hip, fmlp_bwd.hip) take 16-bit io, D in {64, 128} and
+// E % 8 == 0 on dense, 16-byte aligned tensors; everything else within check_shape runs on the
+// generic kernels (fmlp_gen.hip).
+bool tuned_shape(int64_t D, int64_t E, int io) {
+  return (io == FMLP_DTYPE_F16 || io == FMLP_DTYPE_BF16) && (D == 64 || D == 128) && E % 8 == 0;
+}
 
 int check_shape(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   if (H < 0 || B < 0 || D < 0 || E < 0)
     return fail(FMLP_ERR_INVALID_ARG, "negative dimension (H=%lld B=%lld D=%lld E=%lld)", (long long)H,
                 (long long)B, (long long)D, (long long)E);
-  const int io = dtype & ~(FMLP_OUT_F32 | FMLP_DW_HILO);
-  if (io != FMLP_DTYPE_F16 && io != FMLP_DTYPE_BF16)
+  const int io = io_of(dtype);
+  if (io != FMLP_DTYPE_F16 && io != FMLP_DTYPE_BF16 && io != FMLP_DTYPE_F32)
     return fail(FMLP_ERR_UNSUPPORTED,
-                "dtype code %d: only fp16 (0) and bf16 (1) are supported, optionally with FMLP_OUT_F32 / FMLP_DW_HILO",
-                dtype);
-  if (D != 64 && D != 128) return fail(FMLP_ERR_UNSUPPORTED, "hidden dimension D=%lld: supported D are 64 and 128", (long long)D);
-  if (E < 8 || E % 8 != 0)
-    return fail(FMLP_ERR_UNSUPPORTED, "intermediate dimension E=%lld: must be a positive multiple of 8", (long long)E);
+                "dtype code %d: fp16 (0), bf16 (1) or fp32 (2), optionally with FMLP_OUT_F32 / FMLP_DW_HILO", dtype);
+  if (!fmlp::gen_supports_d(D))
+    return fail(FMLP_ERR_UNSUPPORTED, "hidden dimension D=%lld: supported D are 16, 32, 64, 128 and 256", (long long)D);
+  if (E < 1) return fail(FMLP_ERR_UNSUPPORTED, "intermediate dimension E=%lld: must be positive", (long long)E);
   if (B > (1LL << 30) || E > (1LL << 30) || H > (1LL << 30))
     return fail(FMLP_ERR_INVALID_ARG, "dimension too large (H=%lld B=%lld E=%lld)", (long long)H, (long long)B,
                 (long long)E);
-  // the kernels address one head's W1 / W2 (D x E values) with 32-bit byte offsets
-  if (D * E * 2 > 0x7fffffffLL)
-    return fail(FMLP_ERR_UNSUPPORTED, "per-head weight slice D*E=%lld values exceeds 2 GiB", (long long)(D * E));
+  // the tuned kernels address one head's W1 / W2 (D x E values) with 32-bit byte offsets
+  if (D * E * 4 > 0x7fffffffLL)
+    return fail(FMLP_ERR_UNSUPPORTED, "per-head weight slice D*E=%lld values exceeds 512 Mi", (long long)(D * E));
   // every tile count must fit a 32-bit grid
-  if (H * ((B + 127) / 128) + H * ((E + 127) / 128) * 64 > 0x7fffffffLL)
+  if (H * ((B + 127) / 128) + H * ((E + 31) / 32) * 64 > 0x7fffffffLL)
     return fail(FMLP_ERR_INVALID_ARG, "problem too large for one launch");
   return FMLP_OK;
 }
@@ -107,11 +114,56 @@ int check_act(int act) {
   return FMLP_OK;
 }
 
-int check_ptr(const void* p, const char* name, bool needed) {
+// non-NULL and aligned to `align` bytes (16 for the tuned kernels' vector accesses, the
+// element size for the generic kernels)
+int check_ptr(const void* p, const char* name, bool needed, size_t align = 16) {
   if (!needed) return FMLP_OK;
   if (p == nullptr) return fail(FMLP_ERR_INVALID_ARG, "%s is NULL", name);
-  if (!aligned16(p)) return fail(FMLP_ERR_INVALID_ARG, "%s is not 16-byte aligned", name);
+  if ((reinterpret_cast<uintptr_t>(p) % align) != 0)
+    return fail(FMLP_ERR_INVALID_ARG, "%s is not %zu-byte aligned", name, align);
   return FMLP_OK;
+}
+
+// Dense element strides of (n0, n1, n2) row-major.
+void dense3(int64_t n1, int64_t n2, long long* s) {
+  s[0] = (long long)(n1 * n2);
+  s[1] = (long long)n2;
+  s[2] = 1;
+}
+bool is_dense3(const int64_t* s, int64_t n1, int64_t n2) {
+  return s[0] == n1 * n2 && s[1] == n2 && s[2] == 1;
+}
+int check_strides(const int64_t* s, const char* name) {
+  if (s == nullptr) return fail(FMLP_ERR_INVALID_ARG, "%s strides are NULL", name);
+  for (int i = 0; i < 3; ++i)
+    if (s[i] < 0) return fail(FMLP_ERR_INVALID_ARG, "%s stride %d is negative (%lld)", name, i, (long long)s[i]);
+  return FMLP_OK;
+}
+
+fmlp::GenArgs gen_args(const void* x, const void* w1, const void* w2, const void* dout, void* o, void* dx, void* dw1,
+                       void* dw2, int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act) {
+  fmlp::GenArgs g{};
+  g.x = x;
+  g.w1 = w1;
+  g.w2 = w2;
+  g.dout = dout;
+  g.o = o;
+  g.dx = dx;
+  g.dw1 = dw1;
+  g.dw2 = dw2;
+  g.H = H;
+  g.B = B;
+  g.D = D;
+  g.E = E;
+  dense3(B, D, g.sx);
+  dense3(D, E, g.sw1);
+  dense3(E, D, g.sw2);
+  dense3(B, D, g.sdo);
+  g.io = io_of(dtype) == FMLP_DTYPE_F32 ? fmlp::IO_F32 : io_of(dtype) == FMLP_DTYPE_BF16 ? fmlp::IO_BF16 : fmlp::IO_F16;
+  g.act = act;
+  g.out_f32 = (dtype & FMLP_OUT_F32) ? 1 : 0;
+  g.hilo = (dtype & FMLP_DW_HILO) ? 1 : 0;
+  return g;
 }
 
 }  // namespace
@@ -146,26 +198,64 @@ FMLP_EXPORT int fmlp_shape_supported(int64_t H, int64_t B, int64_t D, int64_t E,
   return st == FMLP_OK ? 1 : 0;
 }
 
-FMLP_EXPORT int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
-                         int64_t E, int dtype, int act, void* stream) {
+FMLP_EXPORT int fmlp_shape_tuned(int64_t D, int64_t E, int dtype) { return tuned_shape(D, E, io_of(dtype)) ? 1 : 0; }
+
+namespace {
+
+int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D, int64_t E,
+             const int64_t* sx, const int64_t* sw1, const int64_t* sw2, int dtype, int act, void* stream) {
   if (dtype & FMLP_DW_HILO) return fail(FMLP_ERR_INVALID_ARG, "FMLP_DW_HILO applies to the backward only");
   int st = check_shape(H, B, D, E, dtype);
   if (st) return st;
   if ((st = check_act(act))) return st;
+  if (sx && ((st = check_strides(sx, "x")) || (st = check_strides(sw1, "w1")) || (st = check_strides(sw2, "w2"))))
+    return st;
   const bool rows = H > 0 && B > 0;
   const bool wts = H > 0;
-  if ((st = check_ptr(x, "x", rows)) || (st = check_ptr(w1, "w1", wts)) || (st = check_ptr(w2, "w2", wts)) ||
-      (st = check_ptr(o, "o", rows)))
+  const int io = io_of(dtype);
+  const size_t es = elem_bytes(io);
+  if ((st = check_ptr(x, "x", rows, es)) || (st = check_ptr(w1, "w1", wts, es)) || (st = check_ptr(w2, "w2", wts, es)) ||
+      (st = check_ptr(o, "o", rows, (dtype & FMLP_OUT_F32) ? 4 : es)))
     return st;
   if (!rows) return ok();
-  fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, io_of(dtype) == FMLP_DTYPE_BF16, act, (dtype & FMLP_OUT_F32) != 0};
-  hipError_t e = fmlp::launch_fwd(a, (hipStream_t)stream);
+  const bool dense = sx == nullptr || (is_dense3(sx, B, D) && is_dense3(sw1, D, E) && is_dense3(sw2, E, D));
+  hipError_t e;
+  if (dense && tuned_shape(D, E, io) && aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(o)) {
+    fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, io == FMLP_DTYPE_BF16, act, (dtype & FMLP_OUT_F32) != 0};
+    e = fmlp::launch_fwd(a, (hipStream_t)stream);
+  } else {
+    fmlp::GenArgs g = gen_args(x, w1, w2, nullptr, o, nullptr, nullptr, nullptr, H, B, D, E, dtype, act);
+    if (sx) {
+      for (int i = 0; i < 3; ++i) {
+        g.sx[i] = sx[i];
+        g.sw1[i] = sw1[i];
+        g.sw2[i] = sw2[i];
+      }
+    }
+    e = fmlp::launch_gen_fwd(g, (hipStream_t)stream);
+  }
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
   return ok();
 }
 
+}  // namespace
+
+FMLP_EXPORT int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
+                         int64_t E, int dtype, int act, void* stream) {
+  return fwd_impl(x, w1, w2, o, H, B, D, E, nullptr, nullptr, nullptr, dtype, act, stream);
+}
+
+FMLP_EXPORT int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B,
+                                 int64_t D, int64_t E, const int64_t* x_strides, const int64_t* w1_strides,
+                                 const int64_t* w2_strides, int dtype, int act, void* stream) {
+  if (x_strides == nullptr || w1_strides == nullptr || w2_strides == nullptr)
+    return fail(FMLP_ERR_INVALID_ARG, "stride arrays must not be NULL");
+  return fwd_impl(x, w1, w2, o, H, B, D, E, x_strides, w1_strides, w2_strides, dtype, act, stream);
+}
+
 FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   if (check_shape(H, B, D, E, dtype) != FMLP_OK) return 0;
+  if (!tuned_shape(D, E, io_of(dtype))) return 0;  // the generic kernels need no workspace
   int cus = 0;
   if (num_cus_current(&cus) != FMLP_OK) return 0;
   return fmlp::plan_bwd(H, B, D, E, cus).ws_bytes;
@@ -173,26 +263,70 @@ FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int
 
 namespace {
 
-// Argument checks shared by fmlp_bwd and fmlp_bwd_noalloc; fills the plan when there is
-// work (returns FMLP_OK with *work = false for H == 0).
-int bwd_prepare(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1, void* dw2,
-                int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, fmlp::BwdPlan* plan, bool* work) {
-  *work = false;
+// The backward of every entry point: argument checks, then the tuned kernels (dense, aligned,
+// tuned shape; fp32 partials in `ws`, or in the static scratch when `noalloc`) or the
+// generic kernels.
+int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1, void* dw2,
+             int64_t H, int64_t B, int64_t D, int64_t E, const int64_t* sx, const int64_t* sw1, const int64_t* sw2,
+             const int64_t* sdo, int dtype, int act, void* workspace, size_t workspace_bytes, bool noalloc,
+             void* stream) {
   int st = check_shape(H, B, D, E, dtype);
   if (st) return st;
   if ((st = check_act(act))) return st;
+  if (sx && ((st = check_strides(sx, "x")) || (st = check_strides(sw1, "w1")) || (st = check_strides(sw2, "w2")) ||
+             (st = check_strides(sdo, "dout"))))
+    return st;
   const bool rows = H > 0 && B > 0;
   const bool wts = H > 0;
-  if ((st = check_ptr(x, "x", rows)) || (st = check_ptr(w1, "w1", wts)) || (st = check_ptr(w2, "w2", wts)) ||
-      (st = check_ptr(dout, "dout", rows)) || (st = check_ptr(dx, "dx", rows)) || (st = check_ptr(dw1, "dw1", wts)) ||
-      (st = check_ptr(dw2, "dw2", wts)))
+  const int io = io_of(dtype);
+  const size_t es = elem_bytes(io), os = (dtype & FMLP_OUT_F32) ? 4 : es;
+  if ((st = check_ptr(x, "x", rows, es)) || (st = check_ptr(w1, "w1", wts, es)) || (st = check_ptr(w2, "w2", wts, es)) ||
+      (st = check_ptr(dout, "dout", rows, es)) || (st = check_ptr(dx, "dx", rows, os)) ||
+      (st = check_ptr(dw1, "dw1", wts, os)) || (st = check_ptr(dw2, "dw2", wts, os)))
     return st;
-  if (H == 0) return FMLP_OK;
-  int cus = 0;
-  if ((st = num_cus_current(&cus))) return st;
-  *plan = fmlp::plan_bwd(H, B, D, E, cus);
-  *work = true;
-  return FMLP_OK;
+  if (H == 0) return ok();
+  const bool dense = sx == nullptr || (is_dense3(sx, B, D) && is_dense3(sw1, D, E) && is_dense3(sw2, E, D) &&
+                                       is_dense3(sdo, B, D));
+  const bool aligned = aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(dout) && aligned16(dx) &&
+                       aligned16(dw1) && aligned16(dw2);
+  hipError_t e;
+  if (dense && aligned && tuned_shape(D, E, io)) {
+    int cus = 0;
+    if ((st = num_cus_current(&cus))) return st;
+    const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, cus);
+    void* ws = workspace;
+    if (plan.ws_bytes > 0) {
+      if (noalloc) {
+        if (plan.ws_bytes > fmlp::kScratchBytes)
+          return fail(FMLP_ERR_WORKSPACE,
+                      "fmlp_bwd_noalloc: these shapes need %zu bytes of scratch, the static scratch holds %zu "
+                      "(FMLP_SCRATCH_MAX_BYTES); call fmlp_bwd with a workspace instead",
+                      plan.ws_bytes, fmlp::kScratchBytes);
+        e = fmlp::scratch_current_device(&ws);
+        if (e != hipSuccess) return fail(FMLP_ERR_HIP, "scratch lookup: %s", hipGetErrorString(e));
+      } else {
+        if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
+          return fail(FMLP_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, plan.ws_bytes);
+        if (!aligned16(workspace)) return fail(FMLP_ERR_INVALID_ARG, "workspace is not 16-byte aligned");
+      }
+    }
+    fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io == FMLP_DTYPE_BF16, act, ws,
+                    (dtype & FMLP_OUT_F32) != 0, (dtype & FMLP_DW_HILO) != 0};
+    e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
+  } else {
+    fmlp::GenArgs g = gen_args(x, w1, w2, dout, nullptr, dx, dw1, dw2, H, B, D, E, dtype, act);
+    if (sx) {
+      for (int i = 0; i < 3; ++i) {
+        g.sx[i] = sx[i];
+        g.sw1[i] = sw1[i];
+        g.sw2[i] = sw2[i];
+        g.sdo[i] = sdo[i];
+      }
+    }
+    e = fmlp::launch_gen_bwd(g, (hipStream_t)stream);
+  }
+  if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
+  return ok();
 }
 
 }  // namespace
@@ -200,44 +334,23 @@ int bwd_prepare(const void* x, const void* w1, const void* w2, const void* dout,
 FMLP_EXPORT int fmlp_bwd(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1,
                          void* dw2, int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, void* workspace,
                          size_t workspace_bytes, void* stream) {
-  fmlp::BwdPlan plan{};
-  bool work = false;
-  int st = bwd_prepare(x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, dtype, act, &plan, &work);
-  if (st) return st;
-  if (!work) return ok();
-  if (plan.ws_bytes > 0) {
-    if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
-      return fail(FMLP_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, plan.ws_bytes);
-    if (!aligned16(workspace)) return fail(FMLP_ERR_INVALID_ARG, "workspace is not 16-byte aligned");
-  }
-  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io_of(dtype) == FMLP_DTYPE_BF16, act, workspace,
-                  (dtype & FMLP_OUT_F32) != 0, (dtype & FMLP_DW_HILO) != 0};
-  hipError_t e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
-  if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
-  return ok();
+  return bwd_impl(x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, nullptr, nullptr, nullptr, nullptr, dtype, act, workspace,
+                  workspace_bytes, false, stream);
+}
+
+FMLP_EXPORT int fmlp_bwd_strided(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1,
+                                 void* dw2, int64_t H, int64_t B, int64_t D, int64_t E, const int64_t* x_strides,
+                                 const int64_t* w1_strides, const int64_t* w2_strides, const int64_t* dout_strides,
+                                 int dtype, int act, void* workspace, size_t workspace_bytes, void* stream) {
+  if (x_strides == nullptr || w1_strides == nullptr || w2_strides == nullptr || dout_strides == nullptr)
+    return fail(FMLP_ERR_INVALID_ARG, "stride arrays must not be NULL");
+  return bwd_impl(x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, x_strides, w1_strides, w2_strides, dout_strides, dtype,
+                  act, workspace, workspace_bytes, false, stream);
 }
 
 FMLP_EXPORT int fmlp_bwd_noalloc(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1,
                                  void* dw2, int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act,
                                  void* stream) {
-  fmlp::BwdPlan plan{};
-  bool work = false;
-  int st = bwd_prepare(x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, dtype, act, &plan, &work);
-  if (st) return st;
-  if (!work) return ok();
-  void* scratch = nullptr;
-  if (plan.ws_bytes > 0) {
-    if (plan.ws_bytes > fmlp::kScratchBytes)
-      return fail(FMLP_ERR_WORKSPACE,
-                  "fmlp_bwd_noalloc: these shapes need %zu bytes of scratch, the static scratch holds %zu "
-                  "(FMLP_SCRATCH_MAX_BYTES); call fmlp_bwd with a workspace instead",
-                  plan.ws_bytes, fmlp::kScratchBytes);
-    hipError_t e = fmlp::scratch_current_device(&scratch);
-    if (e != hipSuccess) return fail(FMLP_ERR_HIP, "scratch lookup: %s", hipGetErrorString(e));
-  }
-  fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io_of(dtype) == FMLP_DTYPE_BF16, act, scratch,
-                  (dtype & FMLP_OUT_F32) != 0, (dtype & FMLP_DW_HILO) != 0};
-  hipError_t e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
-  if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
-  return ok();
+  return bwd_impl(x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, nullptr, nullptr, nullptr, nullptr, dtype, act, nullptr, 0,
+                  true, stream);
 }

@@ -59,6 +59,31 @@ struct BwdArgs {
   bool dw_hilo;  // dW products with hi/lo terms of h and dZ (FMLP_DW_HILO)
 };
 
+// io element types of the generic kernels
+enum IoType { IO_F16 = 0, IO_BF16 = 1, IO_F32 = 2 };
+
+// Generic kernels (fmlp_gen.hip): D in {16, 32, 64, 128, 256}, fp16 / bf16 / fp32 io, any E,
+// inputs with arbitrary element strides (head, row, column), dense row-major outputs.
+struct GenArgs {
+  const void* x;
+  const void* w1;
+  const void* w2;
+  const void* dout;
+  void* o;
+  void* dx;
+  void* dw1;
+  void* dw2;
+  long long H, B, D, E;
+  long long sx[3], sw1[3], sw2[3], sdo[3];  // element strides of X (H,B,D), W1 (H,D,E), W2 (H,E,D), dO
+  int io;       // IoType
+  int act;
+  int out_f32;  // outputs as fp32 (FMLP_OUT_F32)
+  int hilo;     // dW products with hi/lo terms of h and dZ (FMLP_DW_HILO; 16-bit io)
+};
+hipError_t launch_gen_fwd(const GenArgs& a, hipStream_t st);
+hipError_t launch_gen_bwd(const GenArgs& a, hipStream_t st);
+bool gen_supports_d(int64_t D);
+
 BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus);
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t st);
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st);

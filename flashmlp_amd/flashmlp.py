@@ -24,7 +24,12 @@ Differences from the reference, all deliberate:
     torch.zeros_like (flashmlp.py:462,516-518);
   * flashmlp_bwd also checks the head counts (flashmlp.py:496-499 omits them);
   * Leaky ReLU's derivative at Z == 0 is autograd's 0.01 (flashmlp.py:33-34 uses 1.0);
-  * io dtypes are fp16 and bf16; other dtypes raise TypeError.
+  * io dtypes are fp16, bf16 and fp32 (fp32 in true fp32, where the reference's tl.dot would
+    use its default reduced input precision); other dtypes raise TypeError;
+  * strided inputs are accepted: shapes the tuned kernels take (16-bit io, D in {64, 128},
+    E % 8 == 0) copy them to dense tensors, as the reference's reshape / contiguous does
+    (flashmlp.py:453-459,508); every other shape reads the views in place (generic kernels),
+    where the reference would copy them or fail its contiguity assertions.
 """
 from __future__ import annotations
 
@@ -36,7 +41,8 @@ import torch
 
 from . import _lib
 
-_DTYPES = {torch.float16: _lib.FMLP_DTYPE_F16, torch.bfloat16: _lib.FMLP_DTYPE_BF16}
+_DTYPES = {torch.float16: _lib.FMLP_DTYPE_F16, torch.bfloat16: _lib.FMLP_DTYPE_BF16,
+           torch.float32: _lib.FMLP_DTYPE_F32}
 
 
 def _act_code(activation: str) -> int:
@@ -50,7 +56,7 @@ def _check_tensors(*ts: torch.Tensor) -> int:
             f"FlashMLP runs on an AMD GPU through HIP; got a tensor on {dev} (move inputs to 'cuda')")
     dt = ts[0].dtype
     if dt not in _DTYPES:
-        raise TypeError(f"FlashMLP supports float16 and bfloat16 inputs, got {dt}")
+        raise TypeError(f"FlashMLP supports float16, bfloat16 and float32 inputs, got {dt}")
     for t in ts[1:]:
         if t.device != dev:
             raise RuntimeError(f"all tensors must be on one device ({dev} vs {t.device})")
@@ -66,9 +72,16 @@ def _ws_bytes(device_index: int, H: int, B: int, D: int, E: int, dtype: int) -> 
     return int(_lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, dtype))
 
 
-def _aligned(t: torch.Tensor) -> torch.Tensor:
-    # the kernels use 16-byte vector accesses; a view at an odd storage offset is copied
+def _dense(t: torch.Tensor) -> torch.Tensor:
+    # the tuned kernels use 16-byte vector accesses on dense tensors: a strided view, or one at
+    # a storage offset that is not a multiple of 16 bytes, is copied
+    t = t.contiguous()
     return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+@functools.lru_cache(maxsize=1024)
+def _tuned(D: int, E: int, dtype: int) -> bool:
+    return bool(_lib.lib().fmlp_shape_tuned(D, E, dtype))
 
 
 def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation: str = "") -> torch.Tensor:
@@ -89,24 +102,21 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
     H, B, D = x.shape
     E = w1.shape[2]
 
-    x = x.reshape(H * B, D)
-    w1 = w1.reshape(D * H, E)
-    w2 = w2.reshape(E * H, D)
-
-    assert x.is_contiguous(), "Input X must be contiguous"
-    assert w1.is_contiguous(), "Weight W1 must be contiguous"
-    assert w2.is_contiguous(), "Weight W2 must be contiguous"
-
     dtype = _check_tensors(x, w1, w2)
-    x, w1, w2 = _aligned(x), _aligned(w1), _aligned(w2)
-    o = torch.empty_like(x)
+    o = torch.empty((H, B, D), dtype=x.dtype, device=x.device)
     L = _lib.lib()
     with torch.cuda.device(x.device):
         stream = torch.cuda.current_stream(x.device).cuda_stream
-        st = L.fmlp_fwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), o.data_ptr(), H, B, D, E, dtype,
-                        _act_code(activation), stream)
+        if _tuned(D, E, dtype):
+            x, w1, w2 = _dense(x), _dense(w1), _dense(w2)
+            st = L.fmlp_fwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), o.data_ptr(), H, B, D, E, dtype,
+                            _act_code(activation), stream)
+        else:
+            st = L.fmlp_fwd_strided(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), o.data_ptr(), H, B, D, E,
+                                    _lib.strides(x), _lib.strides(w1), _lib.strides(w2), dtype,
+                                    _act_code(activation), stream)
     _lib.check(st, "forward")
-    return o.reshape(H, B, D)
+    return o
 
 
 def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.Tensor,
@@ -127,33 +137,29 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     H, B, D = x.shape
     E = w1.shape[2]
 
-    x = x.reshape(H * B, D)
-    w1 = w1.reshape(D * H, E)
-    w2 = w2.reshape(E * H, D)
-    do = do.reshape(H * B, D).contiguous()
-
-    assert x.is_contiguous(), "Input X must be contiguous"
-    assert w1.is_contiguous(), "Weight W1 must be contiguous"
-    assert w2.is_contiguous(), "Weight W2 must be contiguous"
-    assert do.is_contiguous(), "Gradient dO must be contiguous"
-
     dtype = _check_tensors(x, w1, w2, do)
-    x, w1, w2, do = _aligned(x), _aligned(w1), _aligned(w2), _aligned(do)
-    dx = torch.empty_like(x)
-    dw1 = torch.empty_like(w1)
-    dw2 = torch.empty_like(w2)
+    flags = dtype | (_lib.FMLP_DW_HILO if accurate_dw else 0)
+    dx = torch.empty((H, B, D), dtype=x.dtype, device=x.device)
+    dw1 = torch.empty((H, D, E), dtype=x.dtype, device=x.device)
+    dw2 = torch.empty((H, E, D), dtype=x.dtype, device=x.device)
     L = _lib.lib()
     with torch.cuda.device(x.device):
-        ws_bytes = _ws_bytes(x.device.index if x.device.index is not None else torch.cuda.current_device(),
-                             H, B, D, E, dtype)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
         stream = torch.cuda.current_stream(x.device).cuda_stream
-        st = L.fmlp_bwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(), dw1.data_ptr(),
-                        dw2.data_ptr(), H, B, D, E, dtype | (_lib.FMLP_DW_HILO if accurate_dw else 0),
-                        _act_code(activation),
-                        ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+        if _tuned(D, E, dtype):
+            x, w1, w2, do = _dense(x), _dense(w1), _dense(w2), _dense(do)
+            ws_bytes = _ws_bytes(x.device.index if x.device.index is not None else torch.cuda.current_device(),
+                                 H, B, D, E, dtype)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+            st = L.fmlp_bwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(),
+                            dw1.data_ptr(), dw2.data_ptr(), H, B, D, E, flags, _act_code(activation),
+                            ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+        else:
+            st = L.fmlp_bwd_strided(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(),
+                                    dw1.data_ptr(), dw2.data_ptr(), H, B, D, E, _lib.strides(x), _lib.strides(w1),
+                                    _lib.strides(w2), _lib.strides(do), flags, _act_code(activation), None, 0,
+                                    stream)
     _lib.check(st, "backward")
-    return dx.reshape(H, B, D), dw1.reshape(H, D, E), dw2.reshape(H, E, D)
+    return dx, dw1, dw2
 
 
 class FlashMLPFunction(torch.autograd.Function):

@@ -7,9 +7,14 @@
  *
  * Layouts are the reference's (flashmlp.py:1-14, :453-455, :505-508): contiguous row-major
  *   X, O, dO, dX : (H, B, D)      W1, dW1 : (H, D, E)      W2, dW2 : (H, E, D)
- * Element type of every tensor is the io dtype (fp16 or bf16). All pointers are device
- * pointers on the current HIP device, 16-byte aligned. The library never allocates: the
- * caller passes every buffer, including the backward workspace.
+ * (the *_strided entry points take X, W1, W2, dO with arbitrary element strides). Element
+ * type of every tensor is the io dtype (fp16, bf16 or fp32, as the reference's io dtype is
+ * x's, flashmlp.py:87). All pointers are device pointers on the current HIP device, aligned
+ * to their element size. Two kernel sets sit behind the entry points: the tuned gfx950
+ * kernels for 16-bit io, D in {64, 128}, E % 8 == 0 on dense 16-byte aligned tensors
+ * (fmlp_shape_tuned), and generic kernels for every other supported shape, dtype and layout.
+ * The library never allocates: the caller passes every buffer, including the backward
+ * workspace.
  *
  * Calls are asynchronous on the given hipStream_t (NULL = default stream), never
  * synchronise, keep no mutable global state and are reentrant. A non-zero return is one
@@ -36,7 +41,7 @@ typedef enum {
   FMLP_ERR_WORKSPACE = 4    /* workspace smaller than fmlp_bwd_workspace_bytes() */
 } fmlp_status;
 
-typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1 } fmlp_dtype;
+typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1, FMLP_DTYPE_F32 = 2 } fmlp_dtype;
 
 /* OR-ed into the dtype argument of fmlp_fwd / fmlp_bwd: the outputs (o; dx, dw1, dw2) are
  * written as fp32 arrays of the same shapes, holding the fp32-accumulated sums before their
@@ -70,8 +75,15 @@ const char* fmlp_last_error(void);
  * FMLP_ACT_NONE, like the reference's if/elif chain (flashmlp.py:140-147). */
 int fmlp_act_from_name(const char* name);
 
-/* Shapes the kernels support: 1 on success. D in {64, 128}; E % 8 == 0; H, B, E >= 1. */
+/* Shapes the library supports: 1 on success. D in {16, 32, 64, 128, 256} (powers of two
+ * >= 16, as the reference's tl.arange(0, D) requires, flashmlp.py:66,186); E >= 1; H, B >= 0;
+ * dtype fp16, bf16 or fp32 with optional flags. */
 int fmlp_shape_supported(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
+
+/* 1 when the tuned kernels take these shapes (16-bit io, D in {64, 128}, E % 8 == 0) on dense,
+ * 16-byte aligned tensors; other supported shapes, dtypes and layouts run on the generic
+ * kernels. No counterpart in the reference (its Triton kernels are autotuned per shape). */
+int fmlp_shape_tuned(int64_t D, int64_t E, int dtype);
 
 /*
  * Forward: o = act(x @ w1) @ w2 per head, fp32 accumulation, act(.) rounded to the io
@@ -80,6 +92,15 @@ int fmlp_shape_supported(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
  */
 int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
              int64_t E, int dtype, int act, void* stream);
+
+/* fmlp_fwd with X (H,B,D), W1 (H,D,E), W2 (H,E,D) given as strided views: each *_strides is
+ * three non-negative element strides (head, row, column); o stays dense. No counterpart in
+ * the reference, whose wrapper copies such views through reshape / contiguous
+ * (flashmlp.py:453-459): for callers holding sliced or transposed tensors. Dense strides
+ * take the tuned kernels when the shape allows, other strides the generic kernels. */
+int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
+                     int64_t E, const int64_t* x_strides, const int64_t* w1_strides, const int64_t* w2_strides,
+                     int dtype, int act, void* stream);
 
 /* Bytes of device workspace fmlp_bwd needs for these shapes on the current device
  * (0 when none is needed). */
@@ -95,6 +116,14 @@ size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int 
 int fmlp_bwd(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1, void* dw2,
              int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, void* workspace,
              size_t workspace_bytes, void* stream);
+
+/* fmlp_bwd with X, W1, W2 and dout given as strided views (three element strides each, as in
+ * fmlp_fwd_strided); dx, dw1, dw2 stay dense. No counterpart in the reference (its wrapper
+ * copies dout with .contiguous(), flashmlp.py:508). The workspace rule is fmlp_bwd's. */
+int fmlp_bwd_strided(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1,
+                     void* dw2, int64_t H, int64_t B, int64_t D, int64_t E, const int64_t* x_strides,
+                     const int64_t* w1_strides, const int64_t* w2_strides, const int64_t* dout_strides, int dtype,
+                     int act, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Backward without allocation: fmlp_bwd with the workspace replaced by the library's own

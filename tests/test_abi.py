@@ -65,13 +65,19 @@ def test_shape_support(L):
     assert L.fmlp_shape_supported(32, 16384, 128, 1024, 1) == 1
     assert L.fmlp_shape_supported(8, 4097, 64, 2048, 0) == 1
     assert L.fmlp_shape_supported(1, 1, 64, 8, 1) == 1
-    assert L.fmlp_shape_supported(2, 8, 96, 64, 1) == 0   # D
-    assert L.fmlp_shape_supported(2, 8, 64, 12, 1) == 0   # E % 8
-    assert L.fmlp_shape_supported(2, 8, 64, 64, 2) == 0   # dtype
-    # the fp32-output flag is accepted on either io dtype and nothing else
+    assert L.fmlp_shape_supported(2, 8, 96, 64, 1) == 0   # D not a power of two
+    assert L.fmlp_shape_supported(2, 8, 512, 64, 1) == 0  # D above 256
+    for D in (16, 32, 256):                                # the generic kernels' D
+        assert L.fmlp_shape_supported(2, 8, D, 64, 1) == 1
+    assert L.fmlp_shape_supported(2, 8, 64, 12, 1) == 1   # any E (generic kernels when E % 8 != 0)
+    assert L.fmlp_shape_supported(2, 8, 64, 0, 1) == 0    # E = 0
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 2) == 1   # fp32 io
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 3) == 0   # no such dtype
+    # the fp32-output flag is accepted on every io dtype and nothing else
     assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_OUT_F32) == 1
     assert L.fmlp_shape_supported(2, 8, 64, 64, 0 | _lib.FMLP_OUT_F32) == 1
-    assert L.fmlp_shape_supported(2, 8, 64, 64, 2 | _lib.FMLP_OUT_F32) == 0
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 2 | _lib.FMLP_OUT_F32) == 1
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 3 | _lib.FMLP_OUT_F32) == 0
     # so is the backward's hi/lo dW flag, alone or with the fp32-output flag; unknown bits are not
     assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_DW_HILO) == 1
     assert L.fmlp_shape_supported(2, 8, 64, 64, 0 | _lib.FMLP_DW_HILO | _lib.FMLP_OUT_F32) == 1
@@ -79,6 +85,16 @@ def test_shape_support(L):
     assert L.fmlp_shape_supported(-1, 8, 64, 64, 1) == 0
 
 
+def test_shape_tuned(L):
+    # the tuned gfx950 kernels: 16-bit io, D in {64, 128}, E % 8 == 0
+    assert L.fmlp_shape_tuned(128, 1024, 1) == 1 and L.fmlp_shape_tuned(64, 2048, 0) == 1
+    assert L.fmlp_shape_tuned(128, 1024, 1 | _lib.FMLP_OUT_F32 | _lib.FMLP_DW_HILO) == 1
+    assert L.fmlp_shape_tuned(32, 1024, 1) == 0 and L.fmlp_shape_tuned(256, 1024, 1) == 0
+    assert L.fmlp_shape_tuned(128, 1020, 1) == 0 and L.fmlp_shape_tuned(128, 1024, 2) == 0
+
+
+# Every call below carries fake device addresses: each must be rejected (or be a no-op)
+# before any kernel launch, so the file is safe to run on a machine with a GPU.
 def _fwd(L, x=0x1000, w1=0x1000, w2=0x1000, o=0x1000, H=2, B=8, D=64, E=64, dtype=1, act=1):
     return L.fmlp_fwd(x, w1, w2, o, H, B, D, E, dtype, act, None)
 
@@ -87,14 +103,22 @@ def test_forward_argument_validation(L):
     assert _fwd(L, dtype=1 | _lib.FMLP_DW_HILO) == INVALID  # a backward-only flag
     assert _fwd(L, D=96) == UNSUPPORTED
     assert b"D=96" in L.fmlp_last_error()
-    assert _fwd(L, E=20) == UNSUPPORTED
+    assert _fwd(L, E=0) == UNSUPPORTED
     assert _fwd(L, dtype=5) == UNSUPPORTED
     assert _fwd(L, act=7) == INVALID
     assert _fwd(L, H=-2) == INVALID
     assert _fwd(L, x=None) == INVALID
     assert b"x is NULL" in L.fmlp_last_error()
-    assert _fwd(L, w2=0x1008) == INVALID
+    assert _fwd(L, w2=0x1001) == INVALID  # not aligned to its 2-byte elements
     assert b"aligned" in L.fmlp_last_error()
+    assert _fwd(L, dtype=2, w1=0x1002) == INVALID  # fp32 elements need 4-byte alignment
+    # strided entry point: NULL or negative strides are rejected
+    s3 = (ctypes.c_int64 * 3)(512, 64, 1)
+    neg = (ctypes.c_int64 * 3)(512, -64, 1)
+    assert L.fmlp_fwd_strided(0x1000, 0x1000, 0x1000, 0x1000, 2, 8, 64, 64, None, s3, s3, 1, 1, None) == INVALID
+    assert L.fmlp_fwd_strided(0x1000, 0x1000, 0x1000, 0x1000, 2, 8, 64, 64, neg, s3, s3, 1, 1, None) == INVALID
+    assert b"negative" in L.fmlp_last_error()
+    assert L.fmlp_fwd_strided(0x1000, 0x1000, 0x1000, 0x1000, 2, 8, 96, 64, s3, s3, s3, 1, 1, None) == UNSUPPORTED
     # nothing to do: no pointers needed, no GPU touched
     assert _fwd(L, x=None, o=None, B=0) == OK
     assert L.fmlp_last_error() == b""
@@ -109,10 +133,15 @@ def test_backward_argument_validation(L):
         return L.fmlp_bwd(a["x"], a["w1"], a["w2"], a["do"], a["dx"], a["dw1"], a["dw2"], a["H"], a["B"], a["D"],
                           a["E"], a["dtype"], a["act"], a["ws"], a["nws"], None)
 
-    assert bwd(D=32) == UNSUPPORTED
+    assert bwd(D=96) == UNSUPPORTED
     assert bwd(dw1=None) == INVALID
     assert b"dw1" in L.fmlp_last_error()
-    assert bwd(do=0x2004) == INVALID
+    assert bwd(do=0x2003) == INVALID
+    # fp32 outputs (FMLP_OUT_F32) need 4-byte aligned output pointers
+    assert bwd(dx=0x2002, dtype=1 | _lib.FMLP_OUT_F32) == INVALID
+    # the tuned path's workspace rule: a split shape with no workspace is rejected (without a
+    # GPU the CU-count query fails first)
+    assert bwd(H=2, B=8192, D=128, E=128) in (WORKSPACE, HIPERR)
     assert bwd(act=-1) == INVALID
     assert bwd(H=0, x=None, do=None, dx=None) == OK
 

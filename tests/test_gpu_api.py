@@ -86,8 +86,8 @@ def test_module_3d_and_2d_inputs(dtype):
 
 def test_unsupported_dtype_and_device_errors():
     x, w1, w2, _ = make_inputs(2, 8, 64, 64, torch.float32)
-    with pytest.raises(TypeError, match="float16 and bfloat16"):
-        fm.flashmlp_fwd(x.cuda(), w1.cuda(), w2.cuda(), "silu")
+    with pytest.raises(TypeError, match="float16, bfloat16 and float32"):
+        fm.flashmlp_fwd(x.cuda().double(), w1.cuda().double(), w2.cuda().double(), "silu")
     with pytest.raises(TypeError, match="one dtype"):
         fm.flashmlp_fwd(x.cuda().bfloat16(), w1.cuda().half(), w2.cuda().bfloat16(), "silu")
     with pytest.raises(RuntimeError, match="unsupported"):
