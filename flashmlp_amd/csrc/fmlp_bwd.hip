@@ -69,18 +69,22 @@ __device__ __forceinline__ void dw_store(const f32x16 (&a1)[D / 32], const f32x1
       }
     }
   } else {
+    // fp32 partials in the outputs' own layouts (dW2 [h][e][d], dW1 [h][d][e]), so the
+    // reduction is an elementwise sum over the nS slices
     const size_t per = (size_t)H * E * D;
     float* p2 = ws + ((size_t)s * H + h) * E * D;
-    float* p1 = ws + (size_t)nS * per + ((size_t)s * H + h) * E * D;
+    float* p1 = ws + (size_t)nS * per + ((size_t)s * H + h) * D * E;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int e = e0 + 8 * (i >> 2) + 4 * g + (i & 3);
-      if (e < E) {
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int eb = e0 + 8 * i4 + 4 * g;  // 4 consecutive columns eb .. eb+3 (E % 8 == 0)
+      if (eb < E) {
 #pragma unroll
         for (int nt = 0; nt < NTN; ++nt) {
           const int d = nt * 32 + l32;
-          p2[(size_t)e * D + d] = a2[nt][i];
-          p1[(size_t)e * D + d] = a1[nt][i];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) p2[(size_t)(eb + j) * D + d] = a2[nt][4 * i4 + j];
+          const float4 v = {a1[nt][4 * i4], a1[nt][4 * i4 + 1], a1[nt][4 * i4 + 2], a1[nt][4 * i4 + 3]};
+          *(float4*)(p1 + (size_t)d * E + eb) = v;
         }
       }
     }
@@ -933,28 +937,34 @@ dx_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __re
                                       xcd_remap(blockIdx.x, gridDim.x));
 }
 
-// Sum of the nS fp32 partials; dW2 keeps the (e, d) layout, dW1 is written transposed.
+// Sum of the nS fp32 partials (already in dW2's and dW1's layouts), four elements per thread
+// per array; the sum runs in split order, so it is deterministic.
 template <bool BF16>
 __global__ void __launch_bounds__(256)
 dw_reduce_kernel(const float* __restrict__ ws, void* __restrict__ dW1, void* __restrict__ dW2, int H, int E, int D,
                  int nS, int outf32) {
-  const size_t per = (size_t)H * E * D;
+  const size_t per = (size_t)H * E * D;  // a multiple of 8 (E % 8 == 0)
+  const size_t n4 = per / 4;
   const size_t stride = (size_t)gridDim.x * blockDim.x;
-  for (size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x; idx < per; idx += stride) {
-    // dW2[h][e][d]
-    float s2 = 0.f;
-    for (int s = 0; s < nS; ++s) s2 += ws[(size_t)s * per + idx];
-    if (outf32) ((float*)dW2)[idx] = s2;
-    else ((u16*)dW2)[idx] = from_f32<BF16>(s2);
-    // dW1[h][d][e] from ws1[s][h][e][d]
-    const size_t h = idx / ((size_t)D * E);
-    const size_t rem = idx - h * (size_t)D * E;
-    const size_t d = rem / E, e = rem - d * E;
-    const size_t src = (h * E + e) * D + d;
-    float s1 = 0.f;
-    for (int s = 0; s < nS; ++s) s1 += ws[(size_t)(nS + s) * per + src];
-    if (outf32) ((float*)dW1)[idx] = s1;
-    else ((u16*)dW1)[idx] = from_f32<BF16>(s1);
+  for (size_t q = (size_t)blockIdx.x * blockDim.x + threadIdx.x; q < 2 * n4; q += stride) {
+    const bool second = q >= n4;  // 0: dW2 slices, 1: dW1 slices
+    const size_t i = (second ? q - n4 : q) * 4;
+    const float* src = ws + (second ? (size_t)nS * per : 0) + i;
+    float4 acc = *(const float4*)src;
+    for (int s = 1; s < nS; ++s) {
+      const float4 v = *(const float4*)(src + (size_t)s * per);
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    void* dst = second ? dW1 : dW2;
+    if (outf32) {
+      *(float4*)((float*)dst + i) = acc;
+    } else {
+      const u32x2 v = {pack2<BF16>(acc.x, acc.y), pack2<BF16>(acc.z, acc.w)};
+      *(u32x2*)((u16*)dst + i) = v;
+    }
   }
 }
 
@@ -1015,8 +1025,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     e = a.dw_hilo ? launch_u(bwd_kernel<BF16, D, ACT, true>) : launch_u(bwd_kernel<BF16, D, ACT, false>);
     if (e != hipSuccess) return e;
     if (p.nS > 1) {
-      const size_t per = (size_t)a.H * a.E * a.D;
-      size_t blocks = (per + 255) / 256;
+      const size_t items = 2 * ((size_t)a.H * a.E * a.D / 4);
+      size_t blocks = (items + 255) / 256;
       if (blocks > 8192) blocks = 8192;
       hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws,
                          a.dw1, a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
@@ -1039,8 +1049,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     e = a.dw_hilo ? launch_w(dw2_kernel<BF16, D, ACT, true>) : launch_w(dw2_kernel<BF16, D, ACT, false>);
     if (e != hipSuccess) return e;
     if (p.nS > 1) {
-      const size_t per = (size_t)a.H * a.E * a.D;
-      size_t blocks = (per + 255) / 256;
+      const size_t items = 2 * ((size_t)a.H * a.E * a.D / 4);
+      size_t blocks = (items + 255) / 256;
       if (blocks > 8192) blocks = 8192;
       hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws,
                          a.dw1, a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
