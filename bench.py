@@ -200,6 +200,14 @@ def peak_memory(x, w1, w2, do, activation):
     return out
 
 
+def _bwd_splits(H, B, D, E, dt_name):
+    """True when the backward's dW programs split B and a reduction launch follows."""
+    from flashmlp_amd import _lib
+
+    code = _lib.FMLP_DTYPE_BF16 if dt_name == "bf16" else _lib.FMLP_DTYPE_F16
+    return _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, code) > 0
+
+
 def _wall_ms(fn, iters):
     """example.py:65-75: perf_counter around `iters` calls, synchronised at both ends."""
     import torch
@@ -325,6 +333,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-memory", action="store_true", help="skip the peak-memory comparison")
     ap.add_argument("--no-extra", action="store_true", help="skip the autograd-step and host-overhead timings")
+    ap.add_argument("--accurate-dw", action="store_true",
+                    help="time the backward in its dW accuracy mode (h and dZ as hi + lo terms)")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="after timing, run device copies of this size (HBM counter calibration)")
     args = ap.parse_args()
@@ -357,7 +367,7 @@ def main():
     for _ in range(args.warmup):
         fm.flashmlp_fwd(x, w1, w2, act)
         if not fwd_only:
-            fm.flashmlp_bwd(x, w1, w2, do, act)
+            fm.flashmlp_bwd(x, w1, w2, do, act, accurate_dw=args.accurate_dw)
     torch.cuda.synchronize()
 
     K = args.steps
@@ -369,7 +379,7 @@ def main():
         o = fm.flashmlp_fwd(x, w1, w2, act)
         ev[k][1].record()
         if not fwd_only:
-            g = fm.flashmlp_bwd(x, w1, w2, do, act)
+            g = fm.flashmlp_bwd(x, w1, w2, do, act, accurate_dw=args.accurate_dw)
         ev[k][2].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -398,6 +408,8 @@ def main():
         del src, dst
 
     step_name = "fused MLP forward (inference sweep)" if fwd_only else "fused MLP fwd+bwd"
+    if args.accurate_dw:
+        step_name += " (dW accuracy mode)"
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -439,7 +451,9 @@ def main():
         line["bwd_tflops"] = round(bwd_tf, 2)
         line["bwd_hbm_gbs"] = round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1)
         line["roofline"] = {
-            "kernel": "fmlp_bwd call: fmlp::dw2_kernel + fmlp::dx2_kernel",
+            "kernel": "fmlp_bwd call: fmlp::bwd_kernel (dW and dX programs in one launch; problems filling under"
+                      " a quarter of the CUs: dw2_kernel, then dx_kernel)"
+                      + (" + fmlp::dw_reduce_kernel" if _bwd_splits(H, B, D, E, dt_name) else ""),
             "bound": "mfma",
             "achieved": round(bwd_tf, 2),
             "peak": peak,

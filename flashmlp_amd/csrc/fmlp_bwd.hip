@@ -1,13 +1,14 @@
 // FlashMLP backward kernels for gfx950 (MI355X).
 //
-// The reference's two program roles (flashmlp.py:360-373), launched as two kernels so each
-// gets its own register allocation:
-//   * dW programs (dw2_kernel, launched first): per head, 128-column E-tile and B-range;
+// The reference's two program roles (flashmlp.py:360-373). bwd_kernel holds both in one
+// launch, split by workgroup id (dW programs first); problems that fill under a quarter of
+// the CUs launch dw2_kernel, then the 4-wave dx_kernel.
+//   * dW programs (dw2_body): per head, 128-column E-tile and B-range;
 //     recompute Z = X W1c and dH = dO W2c^T per 32-row subtile, then dW2 += h^T dO and
 //     dW1^T += dZ^T X (flashmlp.py:247-329). h and dZ are cast to the io dtype before those
 //     contractions (flashmlp.py:297-320) and come straight from the MFMA C layout
 //     (lane = E column).
-//   * dX programs (dx2_kernel, or dx_kernel for small problems): per head and B-tile;
+//   * dX programs (dx2_body, or dx_role in dx_kernel for small problems): per head and B-tile;
 //     recompute Z^T and dH^T = W2c dO^T per 32-column E-chunk, dZ = dH * act'(Z) cast to the
 //     io dtype, and dX += dZ W1c^T (flashmlp.py:165-244).
 //   * dw_reduce_kernel sums the dW programs' fp32 partials when B is split.
@@ -26,8 +27,8 @@ constexpr int DX_WAVES = 4;
 
 // dW epilogue. C layout of the accumulators: lane = column d
 // (32 nt + l32), rows e = e0 + 8 (i / 4) + 4 g + (i % 4). nS == 1 writes dW1, dW2 in the io
-// dtype (fp32 when outf32); otherwise fp32 partials ws2[s][h][e][d] and ws1[s][h][e][d]
-// (= dW1^T) for dw_reduce_kernel.
+// dtype (fp32 when outf32); otherwise fp32 partials in the outputs' layouts, ws2[s][h][e][d]
+// and ws1[s][h][d][e], which dw_reduce_kernel sums elementwise.
 template <bool BF16, int D>
 __device__ __forceinline__ void dw_store(const f32x16 (&a1)[D / 32], const f32x16 (&a2)[D / 32], void* __restrict__ dW1,
                                          void* __restrict__ dW2, float* __restrict__ ws, int H, int E, int h, int s,
@@ -890,8 +891,7 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
   }
 }
 
-// dX programs: 4 waves; at D = 64 two workgroups share a CU (two waves per SIMD), at
-// D = 128 the role needs more than 256 VGPRs and runs one wave per SIMD.
+// dX programs as their own launch (FMLP_BWD_UNIFIED=0): 8 waves, two per SIMD.
 template <bool BF16, int D, int ACT>
 __global__ void __launch_bounds__(DX2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,

@@ -36,7 +36,7 @@ extern "C" {
 typedef enum {
   FMLP_OK = 0,
   FMLP_ERR_INVALID_ARG = 1, /* shape, pointer, alignment or size out of contract */
-  FMLP_ERR_UNSUPPORTED = 2, /* valid but not implemented (dtype, D, E % 8 != 0) */
+  FMLP_ERR_UNSUPPORTED = 2, /* valid but not implemented (dtype or flags, D, E < 1, D*E too large) */
   FMLP_ERR_HIP = 3,         /* the HIP runtime reported an error */
   FMLP_ERR_WORKSPACE = 4    /* workspace smaller than fmlp_bwd_workspace_bytes() */
 } fmlp_status;
