@@ -15,9 +15,9 @@
 //   * Z^T is produced in the MFMA C layout (lane = column b), which is exactly the A
 //     operand layout of O += h W2c (lane = row b), so h never round-trips through LDS.
 //   * Software pipeline, iteration c:  Z^T(c+1) = W1c(c+1)^T X^T  and  O += h(c-1) W2c(c-1)
-//     on the matrix cores while h(c) = act(Z^T(c)) runs on the VALU. Chunk c+4 is loaded
+//     on the matrix cores while h(c) = act(Z^T(c)) runs on the VALU. Chunk c+5 is loaded
 //     straight into its LDS slot (buffer loads with the LDS destination, no registers and
-//     no LDS store instructions); one barrier per chunk.
+//     no LDS store instructions); one workgroup barrier per two chunks.
 #include "fmlp_device.h"
 #include "fmlp_launch.h"
 #include <type_traits>
@@ -32,7 +32,8 @@ namespace fmlp {
 // 4 D pieces of W1c and of W2c exactly once (NT == 4 D); two waves per SIMD either way.
 __host__ __device__ constexpr int fwd_waves(int D) { return D / 16; }
 constexpr int FWD_NSLOT = 8;  // LDS ring slots (chunks)
-constexpr int FWD_PF = 4;     // chunks loaded ahead
+constexpr int FWD_PF = 4;     // chunks loaded ahead (with one barrier per chunk)
+constexpr int FWD_SB = 2;     // chunk iterations per workgroup barrier
 
 template <bool BF16, int D, int ACT>
 __global__ void __launch_bounds__(fwd_waves(D) * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -44,8 +45,13 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   constexpr int BB = NW * 32;          // rows per workgroup (32 per wave)
   constexpr unsigned SLOT = 128u * D;  // bytes per ring slot: W1c (64*D) + W2c (64*D)
   constexpr unsigned W2OFF = 64u * D;
-  constexpr int NSLOT = FWD_NSLOT, PF = FWD_PF;
-  static_assert(PF >= 2 && PF <= NSLOT - 2 && (NSLOT & (NSLOT - 1)) == 0, "ring");
+  // SB: chunk iterations per workgroup barrier. The loads run SB - 1 chunks further ahead so
+  // that a barrier covers the SB chunks read after it (measured on MI355X at cfg4: SB = 2 is
+  // about 1 % faster than a barrier per chunk).
+  constexpr int SB = FWD_SB;
+  constexpr int NSLOT = FWD_NSLOT, PF = FWD_PF + (SB - 1);
+  static_assert(SB == 1 || SB == 2, "barrier spacing");
+  static_assert(PF >= 2 && PF <= NSLOT - 2 - (SB - 1) && (NSLOT & (NSLOT - 1)) == 0, "ring");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
@@ -79,7 +85,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   // end of a chunk: the LDS stores are retired and visible after the barrier; the loads of
   // the chunk after next stay in flight (their data is waited for where it is stored)
   auto chunk_end = [&]() {
-    wait_vmcnt<2 * (PF - 2)>();          // this wave's pieces of the chunk read next
+    wait_vmcnt<2 * (PF - 1 - SB)>();     // this wave's pieces of the SB chunks read next
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -119,7 +125,11 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   // ---- prologue: chunks 0 .. PF-1 requested, chunk 0 waited for, Z^T(0) ----
 #pragma unroll
   for (int c = 0; c < PF; ++c) dma_chunk(c);
-  chunk_end();
+  wait_vmcnt<2 * (PF - 2)>();  // chunks 0 and 1
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
   // Pipeline state carried between iterations: Z^T of the chunk to activate and h of the
   // previous chunk (A operand of O += h W2c, two K steps). Iterations run in pairs with the
   // two state copies swapping roles, so nothing is copied between iterations.
@@ -136,7 +146,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   // `in` (Z^T(c), h(c-1)) and writing `out` (Z^T(c+1), h(c)). Written as a fixed sequence of
   // steps: each step issues one MFMA, the operand reads of the MFMA two steps later and a
   // share of the activation; sched_barrier keeps the order.
-  auto iter = [&](auto G1, auto G2, int c, St& in, St& out) {
+  auto iter = [&](auto G1, auto G2, auto SYNC, int c, St& in, St& out) {
     constexpr bool DO_G1 = decltype(G1)::value;
     constexpr bool DO_G2 = decltype(G2)::value;
     constexpr int N1 = DO_G1 ? KS : 0, N2 = DO_G2 ? KS : 0, NOPS = N1 + N2;
@@ -182,7 +192,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    chunk_end();
+    if constexpr (decltype(SYNC)::value) chunk_end();
   };
   auto last_gemm2 = [&](const St& st) {
     const unsigned base2 = ((NC - 1) & (NSLOT - 1)) * SLOT;
@@ -201,18 +211,22 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   } else {
     const std::true_type T{};
     const std::false_type F{};
-    iter(T, F, 0, sa, sb);
+    // barriers after iteration 0 and after every second iteration from there (SB = 2), or
+    // after every iteration (SB = 1); the tail iterations read only chunks the last barrier
+    // covered, so with SB = 2 they need none
+    const std::integral_constant<bool, SB == 1> S1{};
+    iter(T, F, T, 0, sa, sb);
     int c = 1;
     for (; c + 2 < NC; c += 2) {
-      iter(T, T, c, sb, sa);
-      iter(T, T, c + 1, sa, sb);
+      iter(T, T, S1, c, sb, sa);
+      iter(T, T, T, c + 1, sa, sb);
     }
     if (c + 2 == NC) {  // one more full iteration, then the last
-      iter(T, T, c, sb, sa);
-      iter(F, T, c + 1, sa, sb);
+      iter(T, T, S1, c, sb, sa);
+      iter(F, T, S1, c + 1, sa, sb);
       last_gemm2(sb);
     } else {            // c == NC - 1
-      iter(F, T, c, sb, sa);
+      iter(F, T, S1, c, sb, sa);
       last_gemm2(sa);
     }
   }
