@@ -316,10 +316,29 @@ def run_mfma_ceiling(args):
         torch.cuda.synchronize()
         ms = _wall_ms(call, max(args.steps, 50))
         res[name] = {"tflops": round(flops / (ms * 1e-3) / 1e12, 1), "ms_per_launch": round(ms, 4)}
+    # the same loop with a kernel's other per-MFMA work added (random operands): LDS reads
+    # feeding the A operand (1 KB per wave per MFMA) and sigmoid-like VALU chains
+    lib.fmlp_ceiling_mix.restype = ctypes.c_int
+    mix_iters = 1000
+    mix_flops = float(grid) * 4 * mix_iters * 16 * 32768
+    mix = {}
+    for lds_reads in (0, 1):
+        for chains in (0, 1, 2):
+            def call_mix():
+                r = lib.fmlp_ceiling_mix(ctypes.c_void_p(out.data_ptr()), mix_iters, lds_reads, chains, grid, st)
+                if r != 0:
+                    raise RuntimeError(f"fmlp_ceiling_mix: hip error {r}")
+            for _ in range(args.warmup + 20):
+                call_mix()
+            torch.cuda.synchronize()
+            ms = _wall_ms(call_mix, max(args.steps, 50))
+            mix[f"lds{lds_reads}_chains{chains}"] = round(mix_flops / (ms * 1e-3) / 1e12, 1)
     peak = PEAK_TFLOPS["bf16"]
     line = {"metric": "sustained bf16 MFMA rate (v_mfma_f32_32x32x16_bf16, register operands)", "workload": "mfma_ceiling",
             "unit": "TFLOP/s", "peak": peak, "random": res["random"], "zero": res["zero"],
             "random_frac_of_peak": round(res["random"]["tflops"] / peak, 4),
+            "with_per_mfma_work": {"unit": "TFLOP/s", "lds": "1 KB LDS read per wave per MFMA (A operand)",
+                                   "chains": "sigmoid-like VALU chains (mul, exp, add, rcp) per MFMA", **mix},
             "config": {"grid": grid, "waves_per_simd": 2, "mfma_per_wave": iters * 4, "chains_per_wave": 4}}
     print(json.dumps(line), flush=True)
 

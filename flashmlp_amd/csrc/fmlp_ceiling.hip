@@ -59,7 +59,77 @@ mfma_ceiling_kernel(float* __restrict__ out, int iters, int zero_data) {
   out[gid] = s;
 }
 
+// Sustained MFMA rate with a kernel's other per-MFMA work added: NL 16-byte-per-lane LDS reads
+// feeding the A operand (1 KB per wave and read, conflict-free, from a 32 KB LDS tile of random
+// bf16) and NV activation-like VALU chains (v_mul, v_exp, v_add, v_rcp, as one sigmoid element)
+// per MFMA. 16 MFMAs per iteration, four accumulators, two waves per SIMD. The rate relative to
+// the plain loop prices LDS traffic and activation math in MFMA time on a power-limited part.
+template <int NL, int NV>
+__global__ void __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+mfma_mix_kernel(float* __restrict__ out, int iters) {
+  __shared__ bf16x8 tile[2048];
+  const unsigned gid = blockIdx.x * kThreads + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  for (int i = threadIdx.x; i < 2048; i += kThreads)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tile[i][j] = rnd_bf16(mix(blockIdx.x * 16384u + i * 8u + j));
+  __syncthreads();
+  bf16x8 a[16], b[16];
+#pragma unroll
+  for (int c = 0; c < 16; ++c)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const unsigned h = mix(gid * 256u + c * 8u + j);
+      a[c][j] = rnd_bf16(h);
+      b[c][j] = rnd_bf16(mix(h));
+    }
+  float v[2] = {0.01f * lane, 0.5f};
+  f32x16 acc[kChains];
+#pragma unroll
+  for (int c = 0; c < kChains; ++c)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[c][i] = 0.f;
+  for (int it = 0; it < iters; ++it) {
+    const int base = lane ^ ((it & 1) << 5);  // loop-variant, so the reads stay in the loop
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+      bf16x8 A = a[s];
+      if constexpr (NL >= 1) A = tile[base + s * 64];
+      acc[s % kChains] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A, b[s], acc[s % kChains], 0, 0, 0);
+#pragma unroll
+      for (int q = 0; q < NV; ++q)
+        v[q] = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v[q] * -1.4426950408889634f));
+    }
+  }
+  float t = v[0] + v[1];
+#pragma unroll
+  for (int c = 0; c < kChains; ++c)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) t += acc[c][i];
+  out[gid] = t;
+}
+
 }  // namespace
+
+// Launches `grid` workgroups of 256 threads, each wave issuing iters * 16 MFMAs with
+// `lds_reads` (0 or 1) LDS reads and `valu_chains` (0, 1 or 2) activation chains per MFMA;
+// `out` holds grid * 256 floats. FLOPs = grid * 4 * iters * 16 * 32768.
+extern "C" __attribute__((visibility("default"))) int fmlp_ceiling_mix(void* out, int iters, int lds_reads,
+                                                                       int valu_chains, int grid, hipStream_t stream) {
+  if (out == nullptr || iters <= 0 || grid <= 0) return (int)hipErrorInvalidValue;
+  float* o = (float*)out;
+  const dim3 g((unsigned)grid), b(kThreads);
+  switch (lds_reads * 3 + valu_chains) {
+    case 0: hipLaunchKernelGGL((mfma_mix_kernel<0, 0>), g, b, 0, stream, o, iters); break;
+    case 1: hipLaunchKernelGGL((mfma_mix_kernel<0, 1>), g, b, 0, stream, o, iters); break;
+    case 2: hipLaunchKernelGGL((mfma_mix_kernel<0, 2>), g, b, 0, stream, o, iters); break;
+    case 3: hipLaunchKernelGGL((mfma_mix_kernel<1, 0>), g, b, 0, stream, o, iters); break;
+    case 4: hipLaunchKernelGGL((mfma_mix_kernel<1, 1>), g, b, 0, stream, o, iters); break;
+    case 5: hipLaunchKernelGGL((mfma_mix_kernel<1, 2>), g, b, 0, stream, o, iters); break;
+    default: return (int)hipErrorInvalidValue;
+  }
+  return (int)hipGetLastError();
+}
 
 // Launches `grid` workgroups of 256 threads, each wave issuing iters * 4 MFMAs; `out` holds
 // grid * 256 floats. Returns the hipError_t of the launch. FLOPs = grid * 4 * iters * 4 * 32768.

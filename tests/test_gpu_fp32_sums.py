@@ -110,6 +110,15 @@ def test_config_sums(name):
     run_sums(name, c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=[0, c.H - 1])
 
 
+MULTI_ROUND = [(8, 8300, 128, 1000, torch.bfloat16, "silu"), (4, 16500, 64, 992, torch.float16, "sigmoid")]
+
+
+@pytest.mark.parametrize("H,B,D,E,dt,act", MULTI_ROUND, ids=[f"H{c[0]}-B{c[1]}-D{c[2]}-E{c[3]}" for c in MULTI_ROUND])
+def test_multi_round_tail_sums(H, B, D, E, dt, act):
+    # more tiles than one round of resident workgroups, with B and E tails
+    run_sums("multi-round", H, B, D, E, dt, act, seed=11, heads=[0, H - 1])
+
+
 def test_config5s_forward_sums():
     # the B = 65536 forward-only sweep: the forward's fp32 sums only
     c = CONFIGS["cfg5s"]

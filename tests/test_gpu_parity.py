@@ -149,6 +149,17 @@ def test_config4_north_star():
     assert res["dw1_fail_vs_fp32"] <= b1 and res["dw2_fail_vs_fp32"] <= b2, res
 
 
+# More tiles than one round of resident workgroups (over 256 at D = 128, over 512 at D = 64
+# on 256 CUs), with a B tail, a partial last E-chunk and an odd number of E-chunks.
+MULTI_ROUND = [(8, 8300, 128, 1000, torch.bfloat16, "silu"), (4, 16500, 64, 992, torch.float16, "sigmoid"),
+               (9, 7500, 128, 520, torch.bfloat16, "leaky_relu")]
+
+
+@pytest.mark.parametrize("H,B,D,E,dt,act", MULTI_ROUND, ids=[f"H{c[0]}-B{c[1]}-D{c[2]}-E{c[3]}" for c in MULTI_ROUND])
+def test_multi_round_tails(H, B, D, E, dt, act):
+    run_case("multi-round", H, B, D, E, dt, act, seed=11, heads=[0, H - 1])
+
+
 @pytest.mark.parametrize("act", ["", "sigmoid"], ids=["linear", "sigmoid"])
 def test_config5s_forward_sweep(act):
     # the fp16 forward-only inference sweep at B = 65536
