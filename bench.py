@@ -470,8 +470,7 @@ def main():
         line["bwd_tflops"] = round(bwd_tf, 2)
         line["bwd_hbm_gbs"] = round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1)
         line["roofline"] = {
-            "kernel": "fmlp_bwd call: fmlp::bwd_kernel (dW and dX programs in one launch; problems filling under"
-                      " a quarter of the CUs: dw2_kernel, then dx_kernel)"
+            "kernel": "fmlp_bwd call: fmlp::bwd_kernel (dW and dX programs in one launch)"
                       + (" + fmlp::dw_reduce_kernel" if _bwd_splits(H, B, D, E, dt_name) else ""),
             "bound": "mfma",
             "achieved": round(bwd_tf, 2),

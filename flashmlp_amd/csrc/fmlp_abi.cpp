@@ -293,7 +293,7 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
   if (dense && aligned && tuned_shape(D, E, io)) {
     int cus = 0;
     if ((st = num_cus_current(&cus))) return st;
-    const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, cus);
+    const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, cus, noalloc ? fmlp::kScratchBytes : (size_t)-1);
     void* ws = workspace;
     if (plan.ws_bytes > 0) {
       if (noalloc) {

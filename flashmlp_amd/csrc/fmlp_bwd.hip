@@ -1,14 +1,13 @@
 // FlashMLP backward kernels for gfx950 (MI355X).
 //
 // The reference's two program roles (flashmlp.py:360-373). bwd_kernel holds both in one
-// launch, split by workgroup id (dW programs first); problems that fill under a quarter of
-// the CUs launch dw2_kernel, then the 4-wave dx_kernel.
+// launch, split by workgroup id (the role with the longer programs first).
 //   * dW programs (dw2_body): per head, 128-column E-tile and B-range;
 //     recompute Z = X W1c and dH = dO W2c^T per 32-row subtile, then dW2 += h^T dO and
 //     dW1^T += dZ^T X (flashmlp.py:247-329). h and dZ are cast to the io dtype before those
 //     contractions (flashmlp.py:297-320) and come straight from the MFMA C layout
 //     (lane = E column).
-//   * dX programs (dx2_body, or dx_role in dx_kernel for small problems): per head and B-tile;
+//   * dX programs (dx2_body): per head and 256-row B-tile;
 //     recompute Z^T and dH^T = W2c dO^T per 32-column E-chunk, dZ = dH * act'(Z) cast to the
 //     io dtype, and dX += dZ W1c^T (flashmlp.py:165-244).
 //   * dw_reduce_kernel sums the dW programs' fp32 partials when B is split.
@@ -22,8 +21,6 @@ namespace fmlp {
 
 constexpr int DW_ET = 128;           // E columns per dW program (32 per wave column group)
 constexpr int DW_BT = 32;            // rows per streamed subtile
-// dX workgroups of the 4-wave form (one wave per SIMD): 128 rows.
-constexpr int DX_WAVES = 4;
 
 // dW epilogue. C layout of the accumulators: lane = column d
 // (32 nt + l32), rows e = e0 + 8 (i / 4) + 4 g + (i % 4). nS == 1 writes dW1, dW2 in the io
@@ -119,254 +116,6 @@ __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], void* __
       }
     }
   }
-}
-
-// ------------------------------------------------------------------------------------
-// dX role
-// ------------------------------------------------------------------------------------
-template <bool BF16, int D, int ACT, int MT, int DXW>
-__device__ __forceinline__ void dx_role(const u16* __restrict__ X, const u16* __restrict__ W1,
-                                        const u16* __restrict__ W2, const u16* __restrict__ dO,
-                                        void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32, int t) {
-  constexpr int KS = D / 16, NTN = D / 32;
-  constexpr int BB = DXW * MT * 32;
-  constexpr unsigned SLOT = 128u * D;
-  constexpr unsigned W2OFF = 64u * D;
-  constexpr int NP = 8 * D;
-  constexpr int PPT = NP / (DXW * 64);
-  static_assert(NP % (2 * (DXW * 64)) == 0, "pieces per thread");
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
-  const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
-  const int NC = (E + 31) >> 5;
-
-  const u16* Xh = X + (size_t)h * B * D;
-  const u16* dOh = dO + (size_t)h * B * D;
-  const u16* W1h = W1 + (size_t)h * D * E;
-  const u16* W2h = W2 + (size_t)h * E * D;
-  const int b_wave = bt * BB + wave * MT * 32;
-
-  // Branch-free buffer loads (as in the forward kernel): W2c rows past E fall outside the
-  // chunk's resource, W1c columns past E get an out-of-range offset, chunks past the last
-  // one are loaded but never used.
-  u32x4 stg[PPT];
-  const unsigned colq = (tid & 3) * 8;
-  unsigned offW1g[PPT / 2], offW2g[PPT / 2];
-#pragma unroll
-  for (int k = 0; k < PPT / 2; ++k) {
-    const unsigned p = tid + k * (DXW * 64);
-    offW1g[k] = (p >> 2) * (unsigned)E * 2u + (p & 3u) * 16u;           // row d, piece q
-    offW2g[k] = (p / (D / 8)) * (D * 2u) + (p % (D / 8)) * 16u;          // row er, piece q
-  }
-  auto load_chunk = [&](int c) {
-    const int lim = E - c * 32;
-    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, D * E * 2 - 64 * c);
-    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
-#pragma unroll
-    for (int k = 0; k < PPT / 2; ++k) {
-      stg[k] = buf_load16(r1, (int)colq < lim ? offW1g[k] : BUF_OOB);
-      stg[PPT / 2 + k] = buf_load16(r2, offW2g[k]);
-    }
-  };
-  auto store_chunk = [&](int slot) {
-    const unsigned base = slot * SLOT;
-#pragma unroll
-    for (int k = 0; k < PPT; ++k) {
-      if (k < PPT / 2) {
-        const int p = tid + k * (DXW * 64);
-        const int d = p >> 2, q = p & 3;
-        u32x2 lo = {stg[k][0], stg[k][1]}, hi = {stg[k][2], stg[k][3]};
-        lds_write8(base + w1c_off(d, 2 * q), lo);
-        lds_write8(base + w1c_off(d, 2 * q + 1), hi);
-      } else {
-        const int p = tid + (k - PPT / 2) * (DXW * 64);
-        const int er = p / (D / 8), q = p % (D / 8);
-        lds_write16(base + W2OFF + w2s_off(er, q), stg[k]);
-      }
-    }
-  };
-
-  // X and dO rows in registers: B operand (lane = row b, 8 consecutive d)
-  u32x4 xr[MT][KS], dr[MT][KS];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int b = b_wave + mt * 32 + l32;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      u32x4 v = {0u, 0u, 0u, 0u}, w = {0u, 0u, 0u, 0u};
-      if (b < B) {
-        v = *(const u32x4*)(Xh + (size_t)b * D + ks * 16 + g * 8);
-        w = *(const u32x4*)(dOh + (size_t)b * D + ks * 16 + g * 8);
-      }
-      xr[mt][ks] = v;
-      dr[mt][ks] = w;
-    }
-  }
-
-  unsigned offA[2][2];  // tr read of W1c (A operand of Z^T)
-#pragma unroll
-  for (int kp = 0; kp < 2; ++kp)
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-      offA[kp][r] = w1c_off(16 * kp + 8 * g + 4 * r + (i16 >> 2), 4 * (G & 1) + (i16 & 3));
-  // row-wise read of W2c (A operand of dH^T): row l32, 16-byte piece 2ks + g = block ks/2, chunk 2(ks%2) + g
-  unsigned offW2[2];
-#pragma unroll
-  for (int kp = 0; kp < 2; ++kp) offW2[kp] = W2OFF + w2s_off(l32, 2 * kp + g);
-  // 8-byte reads of W1c (B operand of dX): row 32nt + l32, unit 4s + 2r + g; the unit swizzle
-  // of row 32nt + l32 equals that of row l32, so nt only adds 32 rows (2048 bytes)
-  unsigned offW1[2][2];
-#pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-    for (int r = 0; r < 2; ++r) offW1[s2][r] = w1c_off(l32, 4 * s2 + 2 * r + g);
-
-  f32x16 acc[MT][NTN];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < NTN; ++nt) acc[mt][nt] = zero16();
-
-  auto gemm_zh = [&](int slot, f32x16 (&z)[MT], f32x16 (&dh)[MT]) {
-    const unsigned base = slot * SLOT;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      z[mt] = zero16();
-      dh[mt] = zero16();
-    }
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const u32x4 A = cat(lds_read_tr(base + offA[ks & 1][0] + (ks >> 1) * 2048u),
-                          lds_read_tr(base + offA[ks & 1][1] + (ks >> 1) * 2048u));
-      const u32x4 A2 = lds_read16(base + offW2[ks & 1] + (ks >> 1) * 2048u);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        z[mt] = mfma<BF16>(A, xr[mt][ks], z[mt]);
-        dh[mt] = mfma<BF16>(A2, dr[mt][ks], dh[mt]);
-      }
-    }
-  };
-  auto gemm_dx = [&](int slot, const u32x4 (&dzA)[MT][2]) {
-    const unsigned base = slot * SLOT;
-#pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) {
-        const u32x4 Bv = cat(lds_read8(base + offW1[s2][0] + nt * 2048u), lds_read8(base + offW1[s2][1] + nt * 2048u));
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma<BF16>(dzA[mt][s2], Bv, acc[mt][nt]);
-      }
-  };
-  auto activate = [&](const f32x16 (&z)[MT], const f32x16 (&dh)[MT], u32x4 (&dzA)[MT][2]) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2)
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-          dzA[mt][s2][w] = pack2<BF16>(act_b<ACT>(z[mt][8 * s2 + 2 * w], dh[mt][8 * s2 + 2 * w]),
-                                       act_b<ACT>(z[mt][8 * s2 + 2 * w + 1], dh[mt][8 * s2 + 2 * w + 1]));
-  };
-
-  load_chunk(0);
-  store_chunk(0);
-  if (NC > 1) {
-    load_chunk(1);
-    store_chunk(1);
-  }
-  load_chunk(2);
-  __syncthreads();
-  // Pipeline state carried between iterations (ping-pong, no copies): Z^T and dH^T of the
-  // chunk to activate and dZ of the previous chunk (A operand of dX += dZ W1c^T).
-  struct St {
-    f32x16 z[MT], dh[MT];
-    u32x4 dz[MT][2];
-  };
-  St sa, sb;
-  gemm_zh(0, sa.z, sa.dh);
-  // Iteration c reads `in` (Z^T, dH^T of chunk c; dZ of chunk c-1) and writes `out`:
-  // recompute Z^T, dH^T of chunk c+1 (group 1), accumulate dX over chunk c-1 (group 2) and
-  // form dZ of chunk c, as a fixed sequence of steps (see the dW role).
-  auto iter = [&](auto G1, auto G2, int c, St& in, St& out) {
-    constexpr bool DO_G1 = decltype(G1)::value;
-    constexpr bool DO_G2 = decltype(G2)::value;
-    constexpr int N1 = DO_G1 ? 2 * KS : 0, N2 = DO_G2 ? 2 * NTN : 0, NOPS = N1 + N2;
-    constexpr int NEL = 16 * MT;
-    constexpr int PD = 2;
-    const unsigned base1 = ((c + 1) & 3) * SLOT, base2 = ((c - 1) & 3) * SLOT;
-    store_chunk((c + 2) & 3);                  // chunk c+2 (loaded during iteration c-1)
-    load_chunk(c + 3);  // chunk c+3 -> registers
-    __builtin_amdgcn_sched_barrier(0);
-    auto fetch = [&](int j) -> u32x4 {
-      const int q = sched_index(j, N1, N2);
-      if (sched_is_g2(j, N1, N2)) {  // dX += dZ W1c^T: B = W1c rows (e-runs of 4)
-        const int s2 = q / NTN, nt = q % NTN;
-        return cat(lds_read8(base2 + offW1[s2][0] + nt * 2048u), lds_read8(base2 + offW1[s2][1] + nt * 2048u));
-      }
-      const int ks = q >> 1;
-      if ((q & 1) == 0)  // Z^T: A = W1c^T (transposed read)
-        return cat(lds_read_tr(base1 + offA[ks & 1][0] + (ks >> 1) * 2048u),
-                   lds_read_tr(base1 + offA[ks & 1][1] + (ks >> 1) * 2048u));
-      return lds_read16(base1 + offW2[ks & 1] + (ks >> 1) * 2048u);  // dH^T: A = W2c rows
-    };
-    float dv[NEL];
-    u32x4 ring[PD + 1];
-#pragma unroll
-    for (int j = 0; j < PD && j < NOPS; ++j) ring[j] = fetch(j);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int j = 0; j < NOPS; ++j) {
-      const u32x4 cur = ring[j % (PD + 1)];
-      if (j + PD < NOPS) ring[(j + PD) % (PD + 1)] = fetch(j + PD);
-      const int q = sched_index(j, N1, N2);
-      if (sched_is_g2(j, N1, N2)) {
-        const int s2 = q / NTN, nt = q % NTN;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma<BF16>(in.dz[mt][s2], cur, acc[mt][nt]);
-      } else {
-        const int ks = q >> 1;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          // ks == 0 starts the chain from a literal zero accumulator
-          if ((q & 1) == 0) out.z[mt] = mfma<BF16>(cur, xr[mt][ks], ks == 0 ? zero16() : out.z[mt]);
-          else out.dh[mt] = mfma<BF16>(cur, dr[mt][ks], ks == 0 ? zero16() : out.dh[mt]);
-        }
-      }
-#pragma unroll
-      for (int e = sched_elem_begin(j, NOPS, NEL); e < sched_elem_begin(j + 1, NOPS, NEL); ++e) {
-        const int mt = e >> 4, i = e & 15;
-        dv[e] = act_b<ACT>(in.z[mt][i], in.dh[mt][i]);
-        if (e & 1) out.dz[mt][i >> 3][(i >> 1) & 3] = pack2<BF16>(dv[e - 1], dv[e]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    __syncthreads();
-  };
-  if (NC == 1) {
-    activate(sa.z, sa.dh, sb.dz);
-    gemm_dx(0, sb.dz);
-  } else {
-    const std::true_type T{};
-    const std::false_type F{};
-    iter(T, F, 0, sa, sb);
-    int c = 1;
-    for (; c + 2 < NC; c += 2) {
-      iter(T, T, c, sb, sa);
-      iter(T, T, c + 1, sa, sb);
-    }
-    if (c + 2 == NC) {
-      iter(T, T, c, sb, sa);
-      iter(F, T, c + 1, sa, sb);
-      gemm_dx((NC - 1) & 3, sb.dz);
-    } else {
-      iter(F, T, c, sb, sa);
-      gemm_dx((NC - 1) & 3, sa.dz);
-    }
-  }
-
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) store_rows<BF16, D>(acc[mt], dX, (size_t)h * B * D, B, b_wave + mt * 32, g, l32, outf32);
 }
 
 // ------------------------------------------------------------------------------------
@@ -908,33 +657,26 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
                          xcd_remap(blockIdx.x, gridDim.x));
 }
 
-// Unified backward launch (flashmlp.py:341-421's program-id split): workgroups
-// [0, n_dw) are dW programs, the rest dX programs, so dX programs start on the CUs that
-// finish their dW programs first. Both roles use 8 waves (two per SIMD); the dynamic LDS
-// is the dW role's (the larger). Each role's tiles are remapped onto XCDs within its own
-// range (exact when n_dw is a multiple of 8).
+// Unified backward launch (flashmlp.py:341-421's program-id split): the role whose programs
+// run longer comes first in workgroup order (dW programs [0, n_dw) then dX programs, or dX
+// first when dx_first), so the shorter programs fill the CUs that finish early. Both roles
+// use 8 waves (two per SIMD); the dynamic LDS is the dW role's (the larger). Each role's
+// tiles are remapped onto XCDs within its own range (exact when its count is a multiple of 8).
 static_assert(DW2_NT == DX2_NT, "both roles run with the same workgroup size");
 template <bool BF16, int D, int ACT, bool HILO>
 __global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dX, void* __restrict__ dW1, void* __restrict__ dW2,
            float* __restrict__ ws, int H, int B, int E, int nE, int nS, int rows_per_split, int n_dw,
-           int dx_tiles_per_head, int outf32) {
-  const int b = blockIdx.x;
-  if (b < n_dw) {
-    dw2_body<BF16, D, ACT, HILO>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32, xcd_remap(b, n_dw));
+           int dx_tiles_per_head, int dx_first, int outf32) {
+  const int b = blockIdx.x, n_dx = (int)gridDim.x - n_dw;
+  const int bw = dx_first ? b - n_dx : b;  // index among the dW programs (< 0 or >= n_dw: a dX program)
+  if (bw >= 0 && bw < n_dw) {
+    dw2_body<BF16, D, ACT, HILO>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32, xcd_remap(bw, n_dw));
   } else {
-    dx2_body<BF16, D, ACT>(X, W1, W2, dO, dX, B, E, dx_tiles_per_head, outf32,
-                           xcd_remap(b - n_dw, (int)gridDim.x - n_dw));
+    const int bx = dx_first ? b : b - n_dw;
+    dx2_body<BF16, D, ACT>(X, W1, W2, dO, dX, B, E, dx_tiles_per_head, outf32, xcd_remap(bx, n_dx));
   }
-}
-
-template <bool BF16, int D, int ACT, int MT>
-__global__ void __launch_bounds__(DX_WAVES * 64)
-dx_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-          const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
-  dx_role<BF16, D, ACT, MT, DX_WAVES>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32,
-                                      xcd_remap(blockIdx.x, gridDim.x));
 }
 
 // Sum of the nS fp32 partials (already in dW2's and dW1's layouts), four elements per thread
@@ -971,47 +713,99 @@ dw_reduce_kernel(const float* __restrict__ ws, void* __restrict__ dW1, void* __r
 // ------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------
-BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus) {
+// Estimated time (us) of the single-launch backward with B split ns ways (rows_per_split
+// rows per dW program), used to choose ns: programs run one per CU with the longer role
+// first, each costing a fixed part plus its MACs at a per-CU rate (a dW program: 4 products
+// over rps x 128 x D; a dX program: 3 over 256 x E x D); a split adds the partial reduction
+// (a launch plus its fp32 traffic). Constants fitted to MI355X timings of the configurations.
+static double est_bwd_us(long long H, long long D, long long E, long long nE, long long ns, long long rps,
+                         long long n_dx, int num_cus) {
+  const double kFixed = 9.0, kMacPerUsCu = 1.6e6, kBytesPerUs = 5.0e6;
+  const double tw = kFixed + (double)rps * 128.0 * D * 4.0 / kMacPerUsCu;
+  const double tx = kFixed + 256.0 * E * D * 3.0 / kMacPerUsCu;
+  const long long n_dw = H * nE * ns, N = num_cus > 0 ? num_cus : 1;
+  const bool w_long = tw >= tx;
+  const double tl = w_long ? tw : tx, ts = w_long ? tx : tw;
+  const long long nl = w_long ? n_dw : n_dx, nsh = w_long ? n_dx : n_dw;
+  double t;
+  if (nl + nsh <= N) {
+    t = nsh > 0 ? (tl > ts ? tl : ts) : tl;
+  } else {
+    const double rounds = (double)((nl + N - 1) / N) * tl;
+    const double spread = ((double)nl * tl + (double)nsh * ts) / (double)N + ts;
+    t = rounds > spread ? rounds : spread;
+  }
+  if (ns > 1) t += 4.0 + (double)(2 * ns + 1) * H * E * D * 4.0 / kBytesPerUs;
+  return t;
+}
+
+BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t max_ws) {
   BwdPlan p{};
   p.nE = (int)((E + DW_ET - 1) / DW_ET);
   const long long base = H * (long long)p.nE;
-  // B splits so that the dW programs alone cover every CU; each split keeps >= 256 rows.
-  long long ns = base > 0 ? (num_cus + base - 1) / base : 1;
+  p.dx_tiles_per_head = (int)((B + DX2_ROWS - 1) / DX2_ROWS);
+  p.n_dx = (long long)p.dx_tiles_per_head * H;
+  // B splits for the dW programs: the candidate (1, 2, 4, ..., at most B / 256 and at most two
+  // dW programs per CU, so the fp32 partials stay within 64 MiB at D <= 128 on 256 CUs) with
+  // the lowest estimated time whose workspace fits max_ws. FMLP_BWD_NS forces a value.
+  static const int ns_env = env_int("FMLP_BWD_NS", 0);
   const long long max_ns = B / 256 > 1 ? B / 256 : 1;
-  if (ns > max_ns) ns = max_ns;
-  if (ns < 1) ns = 1;
-  long long rps = (B + ns - 1) / ns;
-  rps = (rps + DW_BT - 1) / DW_BT * DW_BT;
-  if (rps < DW_BT) rps = DW_BT;
-  ns = (B + rps - 1) / rps;
+  long long cap = base > 0 ? 2LL * num_cus / base : 1;
+  if (cap < 1) cap = 1;
+  if (cap > max_ns) cap = max_ns;
+  auto rows_for = [&](long long ns) {
+    long long rps = (B + ns - 1) / ns;
+    rps = (rps + DW_BT - 1) / DW_BT * DW_BT;
+    return rps < DW_BT ? (long long)DW_BT : rps;
+  };
+  auto ws_for = [&](long long ns) { return ns > 1 ? (size_t)2 * ns * H * E * D * sizeof(float) : (size_t)0; };
+  long long best = 1;
+  if (ns_env > 0) {
+    best = ns_env < max_ns ? ns_env : max_ns;
+  } else {
+    double best_t = est_bwd_us(H, D, E, p.nE, 1, rows_for(1), p.n_dx, num_cus);
+    for (long long ns = 2; ns <= cap; ns *= 2) {
+      const long long rps = rows_for(ns), eff = (B + rps - 1) / rps;
+      if (ws_for(eff) > max_ws) break;
+      const double t = est_bwd_us(H, D, E, p.nE, eff, rps, p.n_dx, num_cus);
+      if (t < best_t) {
+        best_t = t;
+        best = eff;
+      }
+    }
+  }
+  const long long rps = rows_for(best);
+  long long ns = (B + rps - 1) / rps;
   if (ns < 1) ns = 1;
   p.nS = (int)ns;
   p.rows_per_split = (int)rps;
-  // dX programs: the 8-wave form unless it would leave most CUs idle (measured on MI355X:
-  // it wins from about a quarter of the CUs busy, the 4-wave form below that).
-  // FMLP_DX_KIND (read once per process) forces 0 (4-wave) or 1 (8-wave).
-  static const int dx_kind_env = env_int("FMLP_DX_KIND", -1);
-  const long long big = (B + DX2_ROWS - 1) / DX2_ROWS * H;
-  p.dx_mt = 1;
-  p.dx_kind = dx_kind_env >= 0 ? (dx_kind_env ? 1 : 0) : (4 * big >= num_cus ? 1 : 0);
-  const int rows = p.dx_kind ? DX2_ROWS : DX_WAVES * 32 * p.dx_mt;
-  p.dx_tiles_per_head = (int)((B + rows - 1) / rows);
   p.n_dw = base * p.nS;
-  p.n_dx = (long long)p.dx_tiles_per_head * H;
-  p.ws_bytes = p.nS > 1 ? (size_t)2 * p.nS * H * E * D * sizeof(float) : 0;
+  // longest programs first (the same per-program costs as the estimate).
+  // FMLP_BWD_ORDER forces 1 (dW first) or 2 (dX first).
+  static const int order_env = env_int("FMLP_BWD_ORDER", 0);
+  p.dx_first = order_env ? (order_env == 2) : (2LL * p.rows_per_split < 3LL * E);
+  p.ws_bytes = ws_for(p.nS);
   return p;
 }
 
 template <bool BF16, int D, int ACT>
 static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
-  if (p.n_dw > 0x7fffffffLL || p.n_dx > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (p.n_dw > 0x7fffffffLL || p.n_dx > 0x7fffffffLL || p.n_dw + p.n_dx > 0x7fffffffLL) return hipErrorInvalidValue;
   hipError_t e;
-  // FMLP_BWD_UNIFIED (read once per process): 1 (default) = one launch holding both roles
-  // when the dX programs use the 8-wave form, 0 = dW and dX programs as two launches
+  const size_t lds = 1280u * D;  // the dW role's: two weight tiles and three subtile pairs (256 D bytes each)
+  auto reduce = [&]() {          // sum of the dW programs' fp32 partials when B is split
+    if (p.nS <= 1) return hipSuccess;
+    const size_t items = 2 * ((size_t)a.H * a.E * a.D / 4);
+    size_t blocks = (items + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws, a.dw1,
+                       a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
+    return hipGetLastError();
+  };
+  // FMLP_BWD_UNIFIED (read once per process): 1 (default) = one launch holding both roles,
+  // 0 = dW programs (and their reduction), then dX programs, as separate launches
   static const int unified = env_int("FMLP_BWD_UNIFIED", 1);
-  if (unified && p.dx_kind == 1 && p.n_dw > 0 && p.n_dx > 0) {
-    if (p.n_dw + p.n_dx > 0x7fffffffLL) return hipErrorInvalidValue;
-    const size_t lds = 1280u * D;  // the dW role's LDS (the dX role uses the first 512 D bytes)
+  if (unified && p.n_dw > 0 && p.n_dx > 0) {
     auto launch_u = [&](auto k) {
       static std::atomic<unsigned long long> lds_set{0};
       hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
@@ -1019,24 +813,14 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
       hipLaunchKernelGGL(k, dim3((unsigned)(p.n_dw + p.n_dx)), dim3(DW2_NT), lds, st, (const u16*)a.x,
                          (const u16*)a.w1, (const u16*)a.w2, (const u16*)a.dout, a.dx, a.dw1, a.dw2, (float*)a.ws,
                          (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw,
-                         p.dx_tiles_per_head, a.out_f32 ? 1 : 0);
+                         p.dx_tiles_per_head, p.dx_first ? 1 : 0, a.out_f32 ? 1 : 0);
       return hipGetLastError();
     };
     e = a.dw_hilo ? launch_u(bwd_kernel<BF16, D, ACT, true>) : launch_u(bwd_kernel<BF16, D, ACT, false>);
     if (e != hipSuccess) return e;
-    if (p.nS > 1) {
-      const size_t items = 2 * ((size_t)a.H * a.E * a.D / 4);
-      size_t blocks = (items + 255) / 256;
-      if (blocks > 8192) blocks = 8192;
-      hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws,
-                         a.dw1, a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
-      e = hipGetLastError();
-    }
-    return e;
+    return reduce();
   }
-  // dW programs (and their partial reduction), then dX programs, in stream order
   if (p.n_dw > 0) {
-    const size_t lds = 1280u * D;  // two weight tiles (256 D bytes each) + three subtile pairs (256 D each)
     auto launch_w = [&](auto k) {
       static std::atomic<unsigned long long> lds_set{0};
       hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
@@ -1048,41 +832,18 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     };
     e = a.dw_hilo ? launch_w(dw2_kernel<BF16, D, ACT, true>) : launch_w(dw2_kernel<BF16, D, ACT, false>);
     if (e != hipSuccess) return e;
-    if (p.nS > 1) {
-      const size_t items = 2 * ((size_t)a.H * a.E * a.D / 4);
-      size_t blocks = (items + 255) / 256;
-      if (blocks > 8192) blocks = 8192;
-      hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws,
-                         a.dw1, a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
-      e = hipGetLastError();
-      if (e != hipSuccess) return e;
-    }
+    if ((e = reduce()) != hipSuccess) return e;
   }
   if (p.n_dx > 0) {
-    const size_t lds = 4u * 128u * D;
-    auto launch = [&](auto k) {
-      static std::atomic<unsigned long long> lds_set{0};
-      hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
-      if (r != hipSuccess) return r;
-      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(DX_WAVES * 64), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                         (const u16*)a.w2, (const u16*)a.dout, a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head,
-                         a.out_f32 ? 1 : 0);
-      return hipGetLastError();
-    };
-    if (p.dx_kind == 1) {
-      const size_t lds2 = 4u * 128u * D;
-      auto k = dx2_kernel<BF16, D, ACT>;
-      static std::atomic<unsigned long long> lds_set{0};
-      e = set_lds_once((const void*)k, (int)lds2, lds_set);
-      if (e != hipSuccess) return e;
-      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(DX2_NT), lds2, st, (const u16*)a.x, (const u16*)a.w1,
-                         (const u16*)a.w2, (const u16*)a.dout, a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head,
-                         a.out_f32 ? 1 : 0);
-      e = hipGetLastError();
-    } else {
-      e = launch(dx_kernel<BF16, D, ACT, 1>);
-    }
+    const size_t lds_x = 4u * 128u * D;  // four chunk slots
+    auto k = dx2_kernel<BF16, D, ACT>;
+    static std::atomic<unsigned long long> lds_set{0};
+    e = set_lds_once((const void*)k, (int)lds_x, lds_set);
     if (e != hipSuccess) return e;
+    hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(DX2_NT), lds_x, st, (const u16*)a.x, (const u16*)a.w1,
+                       (const u16*)a.w2, (const u16*)a.dout, a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head,
+                       a.out_f32 ? 1 : 0);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   return hipSuccess;
 }

@@ -30,15 +30,14 @@ struct FwdArgs {
 // Backward work decomposition (chosen on the host, see plan_bwd):
 //   dW programs: H * nE * nS, each owning an E-tile of 128 columns and a B-range of
 //                rows_per_split rows (nS > 1 writes fp32 partials to the workspace).
-//                8 waves (two per SIMD), dw2_kernel.
-//   dX programs: H * dx_tiles_per_head, each owning dx_rows rows.
+//   dX programs: H * dx_tiles_per_head, each owning 256 rows.
+//   Both 8 waves (two per SIMD), in one launch (bwd_kernel), the longer role first.
 struct BwdPlan {
   int nE;              // E-tiles of 128 per head
   int nS;              // B splits for the dW programs
   int rows_per_split;  // multiple of 32
-  int dx_mt;           // 32-row M-tiles per wave in dX programs (rows per program = 128 * dx_mt)
-  int dx_kind;         // 0: 4-wave software-pipelined dX programs (128 rows); 1: 8-wave (256 rows)
   int dx_tiles_per_head;
+  bool dx_first;       // single-launch order: dX programs before the dW programs
   long long n_dw, n_dx;
   size_t ws_bytes;     // fp32 partials when nS > 1
 };
@@ -84,7 +83,8 @@ hipError_t launch_gen_fwd(const GenArgs& a, hipStream_t st);
 hipError_t launch_gen_bwd(const GenArgs& a, hipStream_t st);
 bool gen_supports_d(int64_t D);
 
-BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus);
+// max_ws: the largest workspace the caller can provide (fmlp_bwd_noalloc: its static scratch)
+BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t max_ws = (size_t)-1);
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t st);
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st);
 

@@ -11,8 +11,8 @@ Bar: normwise relative error <= 1e-4 per output tensor. What remains besides sum
 order is the rare one-ulp flip of an io-rounded intermediate (h or dZ) whose fp32 value sits
 on a rounding boundary; its share is printed.
 
-The cases cover both dX kernels (4-wave for small problems, 8-wave for large) and both dW
-store paths (direct when one B split suffices, fp32 partials + reduction otherwise).
+The cases cover both dW store paths (direct when one B split suffices, fp32 partials +
+reduction otherwise) and both orders of the single backward launch (dW or dX programs first).
 """
 import ctypes
 import sys
@@ -100,7 +100,11 @@ def test_tail_sums():
 
 
 def test_split_reduction_sums():
-    # 12 x 1024 x 64 x 768: the dW programs split B and reduce fp32 partials
+    # few heads, long B: the dW programs split B (16 ways at 2 x 4096 x 128 x 256 on 256 CUs,
+    # 2 ways at 3 x 700 x 64 x 264) and reduce fp32 partials
+    run_sums("split", 2, 4096, 128, 256, torch.bfloat16, "silu", seed=42)
+    run_sums("split", 3, 700, 64, 264, torch.float16, "sigmoid", seed=43)
+    # the reference's test shape (one split, dX programs first)
     run_sums("ref-test-shape", 12, 1024, 64, 768, torch.bfloat16, "silu", seed=42)
 
 

@@ -62,7 +62,7 @@ def _bwd_noalloc(L, x, w1, w2, do, act):
 
 def test_noalloc_matches_workspace_entry_point_twice():
     L = _lib.lib()
-    # first: the cfg3 shape (B split 4 ways, 33.5 MB of partials); second: smaller
+    # first: the cfg3 shape (B split 2 ways, 16.8 MB of partials); second: smaller
     cases = [(16, 8192, 128, 512, torch.bfloat16, "leaky_relu", 21), (6, 1500, 64, 264, torch.float16, "silu", 22)]
     for H, B, D, E, dt, act, seed in cases:
         _say(f"[noalloc] H={H} B={B} D={D} E={E} {dt} act='{act}' seed={seed}")
