@@ -200,14 +200,6 @@ def peak_memory(x, w1, w2, do, activation):
     return out
 
 
-def _bwd_splits(H, B, D, E, dt_name):
-    """True when the backward's dW programs split B and a reduction launch follows."""
-    from flashmlp_amd import _lib
-
-    code = _lib.FMLP_DTYPE_BF16 if dt_name == "bf16" else _lib.FMLP_DTYPE_F16
-    return _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, code) > 0
-
-
 def _wall_ms(fn, iters):
     """example.py:65-75: perf_counter around `iters` calls, synchronised at both ends."""
     import torch
@@ -470,8 +462,8 @@ def main():
         line["bwd_tflops"] = round(bwd_tf, 2)
         line["bwd_hbm_gbs"] = round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1)
         line["roofline"] = {
-            "kernel": "fmlp_bwd call: fmlp::bwd_kernel (dW and dX programs in one launch)"
-                      + (" + fmlp::dw_reduce_kernel" if _bwd_splits(H, B, D, E, dt_name) else ""),
+            "kernel": "fmlp_bwd call: fmlp::bwd_kernel (dW and dX programs in one launch; then"
+                      " fmlp::dw_reduce_kernel when the dW programs split B)",
             "bound": "mfma",
             "achieved": round(bwd_tf, 2),
             "peak": peak,

@@ -258,7 +258,13 @@ FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int
   if (!tuned_shape(D, E, io_of(dtype))) return 0;  // the generic kernels need no workspace
   int cus = 0;
   if (num_cus_current(&cus) != FMLP_OK) return 0;
-  return fmlp::plan_bwd(H, B, D, E, cus).ws_bytes;
+  // the plan depends on the activation, which this query does not take: the largest over them
+  size_t n = 0;
+  for (int act = 0; act < 4; ++act) {
+    const size_t w = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, cus).ws_bytes;
+    if (w > n) n = w;
+  }
+  return n;
 }
 
 namespace {
@@ -293,7 +299,8 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
   if (dense && aligned && tuned_shape(D, E, io)) {
     int cus = 0;
     if ((st = num_cus_current(&cus))) return st;
-    const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, cus, noalloc ? fmlp::kScratchBytes : (size_t)-1);
+    const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, cus,
+                                              noalloc ? fmlp::kScratchBytes : (size_t)-1);
     void* ws = workspace;
     if (plan.ws_bytes > 0) {
       if (noalloc) {

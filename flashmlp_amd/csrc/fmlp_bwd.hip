@@ -14,6 +14,8 @@
 // Leaky ReLU uses the autograd slope at Z == 0 (0.01); the reference Triton kernel uses 1.
 #include "fmlp_device.h"
 #include "fmlp_launch.h"
+#include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <type_traits>
 
@@ -713,78 +715,138 @@ dw_reduce_kernel(const float* __restrict__ ws, void* __restrict__ dW1, void* __r
 // ------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------
-// Estimated time (us) of the single-launch backward with B split ns ways (rows_per_split
-// rows per dW program), used to choose ns: programs run one per CU with the longer role
-// first, each costing a fixed part plus its MACs at a per-CU rate (a dW program: 4 products
-// over rps x 128 x D; a dX program: 3 over 256 x E x D); a split adds the partial reduction
-// (a launch plus its fp32 traffic). Constants fitted to MI355X timings of the configurations.
-static double est_bwd_us(long long H, long long D, long long E, long long nE, long long ns, long long rps,
-                         long long n_dx, int num_cus) {
-  const double kFixed = 9.0, kMacPerUsCu = 1.6e6, kBytesPerUs = 5.0e6;
-  const double tw = kFixed + (double)rps * 128.0 * D * 4.0 / kMacPerUsCu;
-  const double tx = kFixed + 256.0 * E * D * 3.0 / kMacPerUsCu;
-  const long long n_dw = H * nE * ns, N = num_cus > 0 ? num_cus : 1;
-  const bool w_long = tw >= tx;
-  const double tl = w_long ? tw : tx, ts = w_long ? tx : tw;
-  const long long nl = w_long ? n_dw : n_dx, nsh = w_long ? n_dx : n_dw;
-  double t;
-  if (nl + nsh <= N) {
-    t = nsh > 0 ? (tl > ts ? tl : ts) : tl;
-  } else {
-    const double rounds = (double)((nl + N - 1) / N) * tl;
-    const double spread = ((double)nl * tl + (double)nsh * ts) / (double)N + ts;
-    t = rounds > spread ? rounds : spread;
+// ------------------------------------------------------------------------------------
+// Backward plan. The single launch runs H nE nS dW programs and H ceil(B / 256) dX programs,
+// one per CU at a time, one role after the other in workgroup order. The B split nS and the
+// order come from an estimate of the launch's makespan:
+//   * a program costs a fixed part plus its work at a per-CU rate, the work counted in MAC
+//     equivalents per element of the (rows x E) activation plane: 4 D MACs (6 D with the hi/lo
+//     dW terms) plus the activation's VALU share for a dW program, 3 D plus the activation's
+//     share for a dX program;
+//   * the first role's programs are dealt round-robin, each later program goes to the CU that
+//     frees first (list scheduling);
+//   * nS > 1 adds the partial reduction (a launch plus its fp32 traffic).
+// Constants fitted to MI355X timings of 14 shapes x activations x (order, nS); the choice the
+// estimate makes is within 2.5 % of the best measured one for each of them.
+// ------------------------------------------------------------------------------------
+namespace {
+
+constexpr double kPlanFixedUs = 3.0;      // per program
+constexpr double kPlanRate = 4.5e6;       // MAC equivalents per microsecond per CU
+constexpr double kPlanValuMacs = 20.0;    // MAC equivalents per VALU instruction per element
+constexpr double kPlanHbmBytesPerUs = 5.0e6;
+constexpr double kPlanLaunchUs = 4.0;
+
+// VALU instructions per element of the activation plane (dX role: act'; dW role: act and act')
+double valu_dx(int act) { return act == ACT_SILU ? 8.5 : act == ACT_SIGMOID ? 6.5 : act == ACT_LEAKY ? 3.0 : 1.0; }
+double valu_dw(int act) { return act == ACT_SILU ? 9.0 : act == ACT_SIGMOID ? 7.0 : act == ACT_LEAKY ? 4.0 : 1.5; }
+
+// Completion time of n1 programs of t1 dealt round-robin over N CUs, followed by n2 programs of
+// t2 each started on the first CU to come free. The n2 programs take the n2 earliest of the
+// start slots low + k t2 (the CUs done with the first role at `low`) and high + k t2 (the
+// others); the n2-th slot is found by bisection on the slot count.
+double list_makespan(long long n1, double t1, long long n2, double t2, long long N) {
+  const long long q = n1 / N, r = n1 % N;
+  const double low = (double)q * t1, high = r ? (double)(q + 1) * t1 : low;
+  const double end1 = n1 > 0 ? high : 0.0;
+  if (n2 <= 0) return end1;
+  const double a = (double)(N - r), b = (double)r;
+  auto slots_by = [&](double T) {
+    double c = 0.0;
+    if (T >= low) c += a * (std::floor((T - low) / t2) + 1.0);
+    if (b > 0 && T >= high) c += b * (std::floor((T - high) / t2) + 1.0);
+    return c;
+  };
+  double lo = low, hi = high + (double)n2 * t2;
+  for (int it = 0; it < 64; ++it) {
+    const double mid = 0.5 * (lo + hi);
+    if (slots_by(mid) >= (double)n2) hi = mid;
+    else lo = mid;
   }
-  if (ns > 1) t += 4.0 + (double)(2 * ns + 1) * H * E * D * 4.0 / kBytesPerUs;
-  return t;
+  return std::max(end1, hi + t2);
 }
 
-BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t max_ws) {
+long long rows_for_split(long long B, long long ns) {
+  long long rps = (B + ns - 1) / ns;
+  rps = (rps + DW_BT - 1) / DW_BT * DW_BT;
+  return rps < DW_BT ? (long long)DW_BT : rps;
+}
+
+BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int num_cus, size_t max_ws) {
   BwdPlan p{};
   p.nE = (int)((E + DW_ET - 1) / DW_ET);
-  const long long base = H * (long long)p.nE;
+  const long long base = H * (long long)p.nE, N = num_cus > 0 ? num_cus : 1;
   p.dx_tiles_per_head = (int)((B + DX2_ROWS - 1) / DX2_ROWS);
   p.n_dx = (long long)p.dx_tiles_per_head * H;
-  // B splits for the dW programs: the candidate (1, 2, 4, ..., at most B / 256 and at most two
-  // dW programs per CU, so the fp32 partials stay within 64 MiB at D <= 128 on 256 CUs) with
-  // the lowest estimated time whose workspace fits max_ws. FMLP_BWD_NS forces a value.
-  static const int ns_env = env_int("FMLP_BWD_NS", 0);
+  auto ws_for = [&](long long ns) { return ns > 1 ? (size_t)2 * ns * H * E * D * sizeof(float) : (size_t)0; };
+  const double tx = kPlanFixedUs + 256.0 * E * (3.0 * D + valu_dx(act) * kPlanValuMacs) / kPlanRate;
+  const double w_per_row = 128.0 * ((hilo ? 6.0 : 4.0) * D + valu_dw(act) * kPlanValuMacs) / kPlanRate;
+  // candidates nS = 1, 2, 4, ... up to B / 256 and two dW programs per CU (which keeps the fp32
+  // partials within 64 MiB at D <= 128 on 256 CUs), whose workspace fits max_ws
   const long long max_ns = B / 256 > 1 ? B / 256 : 1;
-  long long cap = base > 0 ? 2LL * num_cus / base : 1;
+  long long cap = base > 0 ? 2 * N / base : 1;
   if (cap < 1) cap = 1;
   if (cap > max_ns) cap = max_ns;
-  auto rows_for = [&](long long ns) {
-    long long rps = (B + ns - 1) / ns;
-    rps = (rps + DW_BT - 1) / DW_BT * DW_BT;
-    return rps < DW_BT ? (long long)DW_BT : rps;
-  };
-  auto ws_for = [&](long long ns) { return ns > 1 ? (size_t)2 * ns * H * E * D * sizeof(float) : (size_t)0; };
-  long long best = 1;
-  if (ns_env > 0) {
-    best = ns_env < max_ns ? ns_env : max_ns;
-  } else {
-    double best_t = est_bwd_us(H, D, E, p.nE, 1, rows_for(1), p.n_dx, num_cus);
-    for (long long ns = 2; ns <= cap; ns *= 2) {
-      const long long rps = rows_for(ns), eff = (B + rps - 1) / rps;
-      if (ws_for(eff) > max_ws) break;
-      const double t = est_bwd_us(H, D, E, p.nE, eff, rps, p.n_dx, num_cus);
-      if (t < best_t) {
+  // FMLP_BWD_NS / FMLP_BWD_ORDER (read once per process) force the split and the order
+  // (1: dW programs first, 2: dX programs first)
+  static const int ns_env = env_int("FMLP_BWD_NS", 0);
+  static const int order_env = env_int("FMLP_BWD_ORDER", 0);
+  double best_t = 0.0;
+  long long best_ns = 1;
+  bool best_dx_first = false;
+  for (long long ns = 1; ns <= (ns_env > 0 ? 1 : cap); ns *= 2) {
+    const long long want = ns_env > 0 ? (ns_env < max_ns ? ns_env : max_ns) : ns;
+    const long long rps = rows_for_split(B, want), eff = B > rps ? (B + rps - 1) / rps : 1;
+    if (eff > 1 && ws_for(eff) > max_ws) break;
+    const double tw = kPlanFixedUs + (double)rps * w_per_row;
+    const long long n_dw = base * eff;
+    const double red = eff > 1 ? kPlanLaunchUs + (double)(2 * eff + 1) * H * E * D * 4.0 / kPlanHbmBytesPerUs : 0.0;
+    for (int o = 1; o <= 2; ++o) {
+      if (order_env && o != order_env) continue;
+      const double t = (o == 1 ? list_makespan(n_dw, tw, p.n_dx, tx, N) : list_makespan(p.n_dx, tx, n_dw, tw, N)) + red;
+      if (best_t == 0.0 || t < best_t) {
         best_t = t;
-        best = eff;
+        best_ns = eff;
+        best_dx_first = o == 2;
       }
     }
   }
-  const long long rps = rows_for(best);
-  long long ns = (B + rps - 1) / rps;
-  if (ns < 1) ns = 1;
-  p.nS = (int)ns;
+  const long long rps = rows_for_split(B, best_ns);
+  p.nS = (int)(B > rps ? (B + rps - 1) / rps : 1);
   p.rows_per_split = (int)rps;
   p.n_dw = base * p.nS;
-  // longest programs first (the same per-program costs as the estimate).
-  // FMLP_BWD_ORDER forces 1 (dW first) or 2 (dX first).
-  static const int order_env = env_int("FMLP_BWD_ORDER", 0);
-  p.dx_first = order_env ? (order_env == 2) : (2LL * p.rows_per_split < 3LL * E);
+  p.dx_first = best_dx_first;
   p.ws_bytes = ws_for(p.nS);
+  return p;
+}
+
+}  // namespace
+
+// Plans are computed once per distinct call shape (a small cache of recent ones).
+BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int num_cus, size_t max_ws) {
+  struct Entry {
+    int64_t H, B, D, E;
+    int act, hilo, cus;
+    size_t max_ws;
+    BwdPlan plan;
+  };
+  static std::mutex mu;
+  static Entry cache[16];
+  static int used = 0, next = 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i) {
+      const Entry& c = cache[i];
+      if (c.H == H && c.B == B && c.D == D && c.E == E && c.act == act && c.hilo == (int)hilo && c.cus == num_cus &&
+          c.max_ws == max_ws)
+        return c.plan;
+    }
+  }
+  const BwdPlan p = make_plan(H, B, D, E, act, hilo, num_cus, max_ws);
+  std::lock_guard<std::mutex> lock(mu);
+  cache[next] = Entry{H, B, D, E, act, (int)hilo, num_cus, max_ws, p};
+  next = (next + 1) % 16;
+  if (used < 16) ++used;
   return p;
 }
 

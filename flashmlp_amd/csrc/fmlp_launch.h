@@ -83,8 +83,10 @@ hipError_t launch_gen_fwd(const GenArgs& a, hipStream_t st);
 hipError_t launch_gen_bwd(const GenArgs& a, hipStream_t st);
 bool gen_supports_d(int64_t D);
 
-// max_ws: the largest workspace the caller can provide (fmlp_bwd_noalloc: its static scratch)
-BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t max_ws = (size_t)-1);
+// act: activation code; hilo: FMLP_DW_HILO; max_ws: the largest workspace the caller can provide
+// (fmlp_bwd_noalloc: its static scratch)
+BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int num_cus,
+                 size_t max_ws = (size_t)-1);
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t st);
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st);
 

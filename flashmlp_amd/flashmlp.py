@@ -67,8 +67,8 @@ def _check_tensors(*ts: torch.Tensor) -> int:
 
 @functools.lru_cache(maxsize=256)
 def _ws_bytes(device_index: int, H: int, B: int, D: int, E: int, dtype: int) -> int:
-    # the backward plan depends only on the shapes and the device's CU count; asked once per
-    # (device, shape) so a call plans the backward only inside fmlp_bwd itself
+    # the backward plan depends only on the shapes, the dW mode flag and the device's CU count;
+    # asked once per (device, shape, flags)
     return int(_lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, dtype))
 
 
@@ -148,7 +148,7 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
         if _tuned(D, E, dtype):
             x, w1, w2, do = _dense(x), _dense(w1), _dense(w2), _dense(do)
             ws_bytes = _ws_bytes(x.device.index if x.device.index is not None else torch.cuda.current_device(),
-                                 H, B, D, E, dtype)
+                                 H, B, D, E, flags)
             ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
             st = L.fmlp_bwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(),
                             dw1.data_ptr(), dw2.data_ptr(), H, B, D, E, flags, _act_code(activation),

@@ -102,8 +102,8 @@ int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int
                      int64_t E, const int64_t* x_strides, const int64_t* w1_strides, const int64_t* w2_strides,
                      int dtype, int act, void* stream);
 
-/* Bytes of device workspace fmlp_bwd needs for these shapes on the current device
- * (0 when none is needed). */
+/* Bytes of device workspace fmlp_bwd needs for these shapes and dtype flags (FMLP_DW_HILO
+ * changes it) on the current device, whatever the activation (0 when none is needed). */
 size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
 /*
