@@ -19,6 +19,10 @@ FMLP_DTYPE_F32 = 2
 FMLP_OUT_F32 = 0x100
 # OR-ed into the backward's dtype code: dW products with hi/lo io-dtype terms of h and dZ
 FMLP_DW_HILO = 0x200
+# OR-ed into the backward's dtype code: the recompute-only form (no stored dZ in the workspace)
+FMLP_BWD_RECOMPUTE = 0x400
+# OR-ed into the backward's dtype code: the stored-dZ form whenever the workspace allows (tests)
+FMLP_BWD_STORE_DZ = 0x800
 ACT_CODES = {"": 0, "silu": 1, "leaky_relu": 2, "sigmoid": 3}
 
 # (name, restype, argtypes) for every symbol include/flashmlp.h declares

@@ -76,7 +76,12 @@ int num_cus_current(int* out) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // io dtype of a dtype argument (its flag bits removed)
-int io_of(int dtype) { return dtype & ~(FMLP_OUT_F32 | FMLP_DW_HILO); }
+int io_of(int dtype) { return dtype & ~(FMLP_OUT_F32 | FMLP_DW_HILO | FMLP_BWD_RECOMPUTE | FMLP_BWD_STORE_DZ); }
+
+// backward form selection from the dtype flags (plan_bwd's dz_mode)
+int dz_mode_of(int dtype) {
+  return (dtype & FMLP_BWD_RECOMPUTE) ? fmlp::DZ_NEVER : (dtype & FMLP_BWD_STORE_DZ) ? fmlp::DZ_FORCE : fmlp::DZ_AUTO;
+}
 size_t elem_bytes(int io) { return io == FMLP_DTYPE_F32 ? 4 : 2; }
 
 // The tuned kernels (fmlp_fwd.hip, fmlp_bwd.hip) take 16-bit io, D in {64, 128} and
@@ -93,7 +98,10 @@ int check_shape(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   const int io = io_of(dtype);
   if (io != FMLP_DTYPE_F16 && io != FMLP_DTYPE_BF16 && io != FMLP_DTYPE_F32)
     return fail(FMLP_ERR_UNSUPPORTED,
-                "dtype code %d: fp16 (0), bf16 (1) or fp32 (2), optionally with FMLP_OUT_F32 / FMLP_DW_HILO", dtype);
+                "dtype code %d: fp16 (0), bf16 (1) or fp32 (2), optionally with FMLP_OUT_F32 / FMLP_DW_HILO / "
+                "FMLP_BWD_RECOMPUTE or FMLP_BWD_STORE_DZ", dtype);
+  if ((dtype & FMLP_BWD_RECOMPUTE) && (dtype & FMLP_BWD_STORE_DZ))
+    return fail(FMLP_ERR_INVALID_ARG, "FMLP_BWD_RECOMPUTE and FMLP_BWD_STORE_DZ exclude each other");
   if (!fmlp::gen_supports_d(D))
     return fail(FMLP_ERR_UNSUPPORTED, "hidden dimension D=%lld: supported D are 16, 32, 64, 128 and 256", (long long)D);
   if (E < 1) return fail(FMLP_ERR_UNSUPPORTED, "intermediate dimension E=%lld: must be positive", (long long)E);
@@ -205,6 +213,8 @@ namespace {
 int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D, int64_t E,
              const int64_t* sx, const int64_t* sw1, const int64_t* sw2, int dtype, int act, void* stream) {
   if (dtype & FMLP_DW_HILO) return fail(FMLP_ERR_INVALID_ARG, "FMLP_DW_HILO applies to the backward only");
+  if (dtype & (FMLP_BWD_RECOMPUTE | FMLP_BWD_STORE_DZ))
+    return fail(FMLP_ERR_INVALID_ARG, "FMLP_BWD_RECOMPUTE / FMLP_BWD_STORE_DZ apply to the backward only");
   int st = check_shape(H, B, D, E, dtype);
   if (st) return st;
   if ((st = check_act(act))) return st;
@@ -261,7 +271,8 @@ FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int
   // the plan depends on the activation, which this query does not take: the largest over them
   size_t n = 0;
   for (int act = 0; act < 4; ++act) {
-    const size_t w = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, cus).ws_bytes;
+    const size_t w =
+        fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus).ws_bytes;
     if (w > n) n = w;
   }
   return n;
@@ -299,7 +310,7 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
   if (dense && aligned && tuned_shape(D, E, io)) {
     int cus = 0;
     if ((st = num_cus_current(&cus))) return st;
-    const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, cus,
+    const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus,
                                               noalloc ? fmlp::kScratchBytes : (size_t)-1);
     void* ws = workspace;
     if (plan.ws_bytes > 0) {

@@ -150,6 +150,9 @@ __device__ __forceinline__ constexpr unsigned sig(unsigned m) {
 constexpr int DX2_NW = 8;
 constexpr int DX2_NT = DX2_NW * 64;
 constexpr int DX2_ROWS = DX2_NW * 32;
+constexpr int DX_NSLOT = 8;  // chunk ring slots (128 D bytes each)
+constexpr int DX_PF = 4;     // chunks requested ahead of the one read
+static_assert(DX_PF <= DX_NSLOT - 2, "a slot is reloaded only after the barrier that retires its last reader");
 
 template <bool BF16, int D, int ACT>
 __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* __restrict__ W1,
@@ -194,23 +197,22 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
       dmaCol[k] = -1;
     }
   }
-  // chunk staging: global -> registers (issued one iteration ahead) -> LDS
-  u32x4 stg[NDMA];
-  auto load_chunk = [&](int c) {
+  // chunk staging: buffer-to-LDS loads DX_PF chunks ahead into a DX_NSLOT-slot ring
+  auto dma_chunk = [&](int c) {
     const int lim = E - c * 32;
-    const Rsrc r1 = make_rsrc(W1h + (size_t)c * 32, D * E * 2 - 64 * c);
-    const Rsrc r2 = make_rsrc(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
+    const int rem = D * E * 2 - 64 * c;
+    const i32x4 r1 = make_rsrc_words(W1h + (size_t)c * 32, rem > 0 ? rem : 0);
+    const i32x4 r2 = make_rsrc_words(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
+    const int slot = (c & (DX_NSLOT - 1)) * (int)SLOT + wave * 1024;
 #pragma unroll
     for (int k = 0; k < NDMA; ++k) {
-      const bool w1 = (unsigned)(k * DX2_NT + wave * 64) < 4u * D;  // wave-uniform
-      const unsigned off = w1 ? (dmaCol[k] < lim ? dmaOff[k] : BUF_OOB) : dmaOff[k];
-      stg[k] = buf_load16(w1 ? r1 : r2, off);
-    }
-  };
-  auto store_chunk = [&](int c) {
-    const int dst = (c & 3) * (int)SLOT + wave * 1024 + lane * 16;
+      // W1c or W2c piece (wave-uniform): word-wise selects keep the loop body one basic block
+      const bool w1 = (unsigned)(k * DX2_NT + wave * 64) < 4u * D;
+      i32x4 rr;
 #pragma unroll
-    for (int k = 0; k < NDMA; ++k) lds_write16(dst + k * DX2_NT * 16, stg[k]);
+      for (int i = 0; i < 4; ++i) rr[i] = __builtin_amdgcn_readfirstlane(w1 ? r1[i] : r2[i]);
+      buf_load16_lds(rr, dmaCol[k] < lim ? dmaOff[k] : BUF_OOB, slot + k * DX2_NT * 16);
+    }
   };
 
   // ---- X and dO rows in registers: B operand (lane = row b, 8 consecutive d) ----
@@ -259,7 +261,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
   auto mfma_phase = [&](auto G2, int c) {
     constexpr bool DO_G2 = decltype(G2)::value;
     constexpr int M2 = DO_G2 ? N2 : 0, NOPS = N1 + M2;
-    const int base1 = (c & 3) * (int)SLOT, base2 = ((c - 1) & 3) * (int)SLOT;
+    const int base1 = (c & (DX_NSLOT - 1)) * (int)SLOT, base2 = ((c - 1) & (DX_NSLOT - 1)) * (int)SLOT;
     auto fetch = [&](int j) -> u32x4 {
       const int q = sched_index(j, N1, M2);
       if (sched_is_g2(j, N1, M2)) {
@@ -292,7 +294,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
     }
   };
   auto g2_only = [&](int c) {  // dX += dZ(c) W1c(c)^T
-    const int base2 = (c & 3) * (int)SLOT;
+    const int base2 = (c & (DX_NSLOT - 1)) * (int)SLOT;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
@@ -307,23 +309,20 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
                                 act_b<ACT>(z[8 * s2 + 2 * w + 1], dh[8 * s2 + 2 * w + 1]));
     __builtin_amdgcn_sched_barrier(0);
   };
-  // iteration c stores chunk c + 1 (loaded during iteration c - 1) into its slot and loads
-  // chunk c + 2; the end-of-chunk barrier publishes the stores (their LDS writes retired)
-  // and retires every read of the slot they reuse
-  auto chunk_begin = [&](int c) {
-    store_chunk(c + 1);
-    load_chunk(c + 2);
-  };
+  // iteration c requests chunk c + DX_PF; the end-of-chunk barrier publishes chunk c + 1 (each
+  // wave waits for its own pieces first) and retires every read of chunk c - 1, whose slot
+  // holds chunk c - 1 + DX_NSLOT later
+  auto chunk_begin = [&](int c) { dma_chunk(c + DX_PF); };
   auto chunk_end = [&]() {
+    wait_vmcnt<NDMA * (DX_PF - 1)>();
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     asm volatile("" ::: "memory");       // keep LDS accesses on their side of the barrier
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
 
-  load_chunk(0);
-  store_chunk(0);
-  load_chunk(1);
+#pragma unroll
+  for (int c = 0; c < DX_PF; ++c) dma_chunk(c);
   chunk_end();
   const std::true_type T{};
   const std::false_type F{};
@@ -351,6 +350,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
     valu_phase();
   }
   g2_only(NC - 1);
+  wait_vmcnt<0>();  // chunk loads past the last are still landing (as zeros)
   store_rows<BF16, D>(acc, dX, (size_t)h * B * D, B, b_wave, g, l32, outf32);
 }
 
@@ -381,12 +381,16 @@ __device__ __forceinline__ unsigned wt_off(unsigned r, unsigned q) {
 // lo = round(v - hi), instead of round(v) alone (twice the dW MFMAs, same operand reads);
 // an accuracy mode with no counterpart in the reference, whose kernel rounds h and dZ to
 // the io dtype (flashmlp.py:297-320).
-template <bool BF16, int D, int ACT, bool HILO>
+// DZ: the programs also store dZ (the io-dtype value the dX product takes) to dzt in the image
+// dxg_kernel streams into LDS: [h][b / 256][e / 32][(b % 256) / 32][e % 32][32 positions], row
+// b at position sig(b % 32) (bits 2 and 3 swapped), so each 32-column chunk of a 256-row tile
+// is 16 contiguous KB.
+template <bool BF16, int D, int ACT, bool HILO, bool DZ = false>
 __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* __restrict__ W1,
                                          const u16* __restrict__ W2, const u16* __restrict__ dO,
                                          void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
                                          int H, int B, int E, int nE, int nS, int rows_per_split, int outf32,
-                                         int t) {
+                                         int t, u16* __restrict__ dzt = nullptr, int Bp = 0) {
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr int SUB = 64 * D;            // bytes of a [32][D] subtile
   constexpr int PAIR = 4 * SUB;          // X set0, dO set0, X set1, dO set1
@@ -517,7 +521,10 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
   // over it (its pair is in `slot`). Elements 0-7 (the K-step-0 operands) are activated
   // first; the 8 K-step-0 MFMAs then run with elements 8-15 spread between them, and the
   // 8 K-step-1 MFMAs follow.
-  auto ag2_phase = [&](int slot) {
+  // per-head dZ resource (DZ): Bp / 256 tiles of [nE * 128 rows e][256 positions]
+  const int Ep = nE * DW_ET;
+  const Rsrc rdz = make_rsrc(DZ ? dzt + (size_t)h * Ep * Bp : nullptr, DZ ? Ep * Bp * 2 : 0);
+  auto ag2_phase = [&](int slot, int rbase) {
     const int base2 = RING_OFF + slot * PAIR;
     auto fetch = [&](int q) -> u32x4 {  // (s, nt, which): which 0 -> dW2 (B = dO^T), 1 -> dW1^T (B = X^T)
       const int s2 = q / (2 * NTN), nt = (q % (2 * NTN)) >> 1, which = q & 1;
@@ -560,19 +567,35 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
         if (e < 16) act_elem(e, hv, dv);
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (DZ) {
+      // dzT[s] holds rows 16 s + 4 g + 0..3 and 16 s + 8 + 4 g + 0..3 of column e0 + l32: positions
+      // 16 s + 8 g .. + 7 under sig, one 16-byte store each; subtiles past the program's rows
+      // (the odd last one of a B range) store nothing (out-of-range offset)
+      const bool live = rbase < b_hi;
+      const unsigned blk = ((unsigned)(rbase >> 8) * (unsigned)(Ep >> 5) + (unsigned)(e0 >> 5)) * 8u +
+                           (unsigned)((rbase & 255) >> 5);
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const unsigned off = ((blk * 32u + (unsigned)l32) * 32u + (unsigned)(16 * s2 + 8 * g)) * 2u;
+        __builtin_amdgcn_raw_buffer_store_b128(dzT[s2], rdz, live ? off : BUF_OOB, 0, 0);
+      }
+    }
   };
   // end of a pair: this wave's loads of the next pair have landed; the barrier publishes
   // them and retires every read of the slot the pair after reuses
-  auto pair_end = [&]() {
-    wait_vmcnt<0>();
+  // (DZ: the two dZ stores of the ag2 phase issued after those loads may stay in flight)
+  auto pair_end = [&](auto AFTER_AG2) {
+    wait_vmcnt<(DZ && decltype(AFTER_AG2)::value) ? 2 : 0>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
 
+  const std::true_type AG{};
+  const std::false_type NOAG{};
   if (npair > 0) {
     issue_pair(0, 0);
-    pair_end();  // also publishes the weight tiles
+    pair_end(NOAG);  // also publishes the weight tiles
     int cur = 0, prev = 2, next = 1;  // ring slots of pairs i, i - 1, i + 1
     auto rotate = [&]() {
       const int tmp = prev;
@@ -582,26 +605,28 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
     };
     issue_pair(1, next);
     g1_phase(cur);
+    // first row of the subtile set `set` takes in pair i
+    auto row0 = [&](int i) { return b_lo + (2 * i + set) * DW_BT; };
     if (set == 0) {
-      ag2_phase(cur);
-      pair_end();
+      ag2_phase(cur, row0(0));
+      pair_end(AG);
       for (int i = 1; i < npair; ++i) {
         rotate();
         issue_pair(i + 1, next);
         g1_phase(cur);
-        ag2_phase(cur);
-        pair_end();
+        ag2_phase(cur, row0(i));
+        pair_end(AG);
       }
     } else {
-      pair_end();
+      pair_end(NOAG);
       for (int i = 1; i < npair; ++i) {
         rotate();
         issue_pair(i + 1, next);
-        ag2_phase(prev);
+        ag2_phase(prev, row0(i - 1));
         g1_phase(cur);
-        pair_end();
+        pair_end(AG);
       }
-      ag2_phase(cur);
+      ag2_phase(cur, row0(npair - 1));
     }
   } else {
     wait_vmcnt<0>();
@@ -650,13 +675,13 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   dx2_body<BF16, D, ACT>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32, xcd_remap(blockIdx.x, gridDim.x));
 }
 
-template <bool BF16, int D, int ACT, bool HILO>
+template <bool BF16, int D, int ACT, bool HILO, bool DZ>
 __global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
-           int H, int B, int E, int nE, int nS, int rows_per_split, int outf32) {
-  dw2_body<BF16, D, ACT, HILO>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32,
-                         xcd_remap(blockIdx.x, gridDim.x));
+           int H, int B, int E, int nE, int nS, int rows_per_split, int outf32, u16* __restrict__ dzt, int Bp) {
+  dw2_body<BF16, D, ACT, HILO, DZ>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32,
+                                   xcd_remap(blockIdx.x, gridDim.x), dzt, Bp);
 }
 
 // Unified backward launch (flashmlp.py:341-421's program-id split): the role whose programs
@@ -713,6 +738,180 @@ dw_reduce_kernel(const float* __restrict__ ws, void* __restrict__ dW1, void* __r
 }
 
 // ------------------------------------------------------------------------------------
+// dX from the stored dZ (dxg_kernel): dX = dZ W1^T per head, a GEMM over E, when the dW
+// programs store dZ (the io-dtype value the reference's dX product takes,
+// flashmlp.py:227-235) instead of the dX programs recomputing Z and dH. A tile is 256 rows
+// of one head (one contiguous block of dZ, chunk after chunk), 8 waves x 32 rows; per 32-column
+// E-chunk c a wave issues D/16 MFMAs dX += dZ(c) W1c(c)^T.
+// Persistent: one workgroup per CU walks its tiles as one stream of (tile, chunk) steps, so
+// the loads run ahead across tile boundaries and no tile pays the memory latency up front.
+// LDS: a ring of dZ chunks (8 blocks [32 e][32 positions], 64-byte rows; block w = wave w's
+// rows, read with ds_read_b64_tr_b16 like a row-major [e][b] tile) streamed from HBM 7 steps
+// ahead, and a ring of W1c chunks ([D][32], 64-byte rows, 16-byte chunk q of row r at
+// q ^ ((r >> 2) & 3), read row-wise; L2-resident) 3 steps ahead. One barrier per step.
+// Stored positions are sig-permuted within 16 rows, so C-layout row m is row sig(m).
+// ------------------------------------------------------------------------------------
+constexpr int DXG_ZS = 8;  // dZ chunk ring slots (16 KB each)
+constexpr int DXG_ZPF = 7; // dZ chunks requested ahead: step j + 7 reuses the slot of step j - 1
+constexpr int DXG_WS = 4;  // W1c ring slots (64 D bytes each)
+constexpr int DXG_WPF = 3;
+static_assert(DXG_ZPF <= DXG_ZS - 1 && DXG_WPF <= DXG_WS - 1 && DXG_WPF <= DXG_ZPF, "rings");
+
+template <bool BF16, int D>
+__global__ void __launch_bounds__(DX2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
+dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __restrict__ dX, int B, int Bp, int E,
+           int Ep, int tiles_per_head, int n_tiles, int outf32) {
+  constexpr int NTN = D / 32;
+  constexpr int ZT = 32 * 256 * 2;      // dZ chunk bytes
+  constexpr int WOFF = DXG_ZS * ZT;     // W1c ring after the dZ ring
+  constexpr int WT = 64 * D;            // W1c chunk bytes
+  constexpr int NZ = ZT / 16 / DX2_NT;  // dZ pieces per lane per chunk (2)
+  constexpr int W1W = D / 16;           // waves whose lanes cover W1c's 4 D pieces once (the rest repeat them)
+  static_assert(NZ * 16 * DX2_NT == ZT, "dZ pieces");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
+  const int NC = (E + 31) >> 5;
+  const int nwg = (int)gridDim.x, wg = (int)blockIdx.x;
+  const int my_tiles = wg < n_tiles ? (n_tiles - 1 - wg) / nwg + 1 : 0;
+  const int steps = my_tiles * NC;
+  // tile k of this workgroup: virtual index k * nwg + wg (dispatch order: XCD = index % 8, as
+  // nwg is a multiple of 8), remapped so each XCD walks a contiguous range of tiles (heads)
+  auto tile_of = [&](int k) { return xcd_remap(k * nwg + wg, n_tiles); };
+
+  // dZ piece p = k * 512 + 64 wave + lane: the chunk is stored as its LDS image, 16 p either way
+  unsigned zOff[NZ];
+#pragma unroll
+  for (int k = 0; k < NZ; ++k) zOff[k] = (unsigned)(k * DX2_NT + wave * 64 + lane) * 16u;
+  // W1c piece p = 64 (wave % W1W) + lane: row r = p / 4, logical chunk q = (p % 4) ^ ((r / 4) % 4)
+  const unsigned pw = (unsigned)(wave % W1W) * 64u + lane;
+  const unsigned wr = pw >> 2, wq = (pw & 3u) ^ ((wr >> 2) & 3u);
+  const unsigned wOff = wr * (unsigned)E * 2u + wq * 16u;
+  const int wCol = (int)(wq * 8u);
+
+  // step j = (tile k, chunk c) of this workgroup; steps past the last load nothing (zero-size
+  // resources), so every step issues the same number of loads and the vmcnt waits stay exact.
+  // Each request stream keeps its own cursor; the tile's addresses change only between tiles.
+  struct Cursor {
+    int j, k, c;
+    const u16* z;  // dZ chunk c of tile k
+    const u16* w;  // W1 columns 32 c .. of tile k's head
+  };
+  auto seek = [&](Cursor& q) {  // q.k changed: the new tile's base addresses
+    const int t = q.k < my_tiles ? tile_of(q.k) : 0;
+    const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
+    q.z = dzt + ((size_t)h * Bp + (size_t)bt * DX2_ROWS) * Ep;  // the tile's chunks, 8192 elements each
+    q.w = W1 + (size_t)h * D * E;
+  };
+  auto advance = [&](Cursor& q) {
+    ++q.j;
+    if (++q.c == NC) {
+      q.c = 0;
+      ++q.k;
+      seek(q);
+    } else {
+      q.z += 32 * 256;
+      q.w += 32;
+    }
+  };
+  auto dma_z = [&](const Cursor& q) {
+    const i32x4 rz = make_rsrc_words(q.z, q.k < my_tiles ? 32 * 512 : 0);
+    const int base = (q.j & (DXG_ZS - 1)) * ZT;
+#pragma unroll
+    for (int i = 0; i < NZ; ++i) buf_load16_lds(rz, zOff[i], base + (i * DX2_NT + wave * 64) * 16);
+  };
+  auto dma_w = [&](const Cursor& q) {
+    const int lim = E - q.c * 32;
+    const int rem = D * E * 2 - 64 * q.c;
+    const i32x4 rw = make_rsrc_words(q.w, q.k < my_tiles && rem > 0 ? rem : 0);
+    buf_load16_lds(rw, wCol < lim ? wOff : BUF_OOB, WOFF + (q.j & (DXG_WS - 1)) * WT + (wave % W1W) * 1024);
+  };
+
+  // A operand (dZ, rows = this wave's 32 positions, k = 16 s + 8 g + j): two transposed reads
+  // of block `wave`; B operand (W1c row 32 nt + l32, piece 2 s + g)
+  const int laneA = wave * 2048 + (8 * g + (i16 >> 2)) * 64 + 32 * (G & 1) + 8 * (i16 & 3);
+  int offB[2];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) offB[s2] = WOFF + l32 * 64 + (((2 * s2 + g) ^ ((l32 >> 2) & 3)) << 4);
+
+  f32x16 acc[NTN];
+#pragma unroll
+  for (int nt = 0; nt < NTN; ++nt) acc[nt] = zero16();
+
+  // step i requests dZ of step i + DXG_ZPF, then W1c of step i + DXG_WPF; the prologue runs the
+  // same order for i < 0, so at step j the loads issued after W1c(j) are those of steps
+  // j - 2 .. j - 1 (DXG_WPF - 1 of them)
+  Cursor qz{0, 0, 0, nullptr, nullptr};
+  seek(qz);
+  Cursor qw = qz;
+#pragma unroll
+  for (int i = -DXG_ZPF; i < 0; ++i) {
+    dma_z(qz);
+    advance(qz);
+    if (i + DXG_WPF >= 0) {
+      dma_w(qw);
+      advance(qw);
+    }
+  }
+  int c = 0, k = 0;  // chunk and tile of step j
+  for (int j = 0; j < steps; ++j) {
+    wait_vmcnt<(NZ + 1) * (DXG_WPF - 1)>();  // this wave's pieces of step j (dZ and W1c)
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();  // step j visible; step j - 1 no longer read
+    asm volatile("" ::: "memory");
+    dma_z(qz);
+    advance(qz);
+    dma_w(qw);
+    advance(qw);
+    const int zb = (j & (DXG_ZS - 1)) * ZT, wb = (j & (DXG_WS - 1)) * WT;
+    u32x4 a[2], b[2][NTN];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      a[s2] = cat(lds_read_tr(zb + laneA + s2 * 1024), lds_read_tr(zb + laneA + s2 * 1024 + 256));
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) b[s2][nt] = lds_read16(wb + offB[s2] + nt * 2048);
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) acc[nt] = mfma<BF16>(a[s2], b[s2][nt], acc[nt]);
+    if (++c == NC) {  // tile done: store its rows (C layout: lane = column d, position m -> row sig(m))
+      const int t = tile_of(k);  // once per tile
+      const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
+      const int b_wave = bt * DX2_ROWS + wave * 32;
+      if (outf32) {
+        float* o = (float*)dX + (size_t)h * B * D;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int b = b_wave + (int)sig(8 * (i >> 2) + 4 * g + (i & 3));
+          if (b < B) {
+#pragma unroll
+            for (int nt = 0; nt < NTN; ++nt) o[(size_t)b * D + nt * 32 + l32] = acc[nt][i];
+          }
+        }
+      } else {
+        u16* o = (u16*)dX + (size_t)h * B * D;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int b = b_wave + (int)sig(8 * (i >> 2) + 4 * g + (i & 3));
+          if (b < B) {
+#pragma unroll
+            for (int nt = 0; nt < NTN; ++nt) o[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(acc[nt][i]);
+          }
+        }
+      }
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt) acc[nt] = zero16();
+      c = 0;
+      ++k;
+    }
+  }
+  wait_vmcnt<0>();  // loads past the last step are still landing
+}
+
+// ------------------------------------------------------------------------------------
 // host side
 // ------------------------------------------------------------------------------------
 // ------------------------------------------------------------------------------------
@@ -736,6 +935,8 @@ constexpr double kPlanRate = 4.5e6;       // MAC equivalents per microsecond per
 constexpr double kPlanValuMacs = 20.0;    // MAC equivalents per VALU instruction per element
 constexpr double kPlanHbmBytesPerUs = 5.0e6;
 constexpr double kPlanLaunchUs = 4.0;
+constexpr double kPlanDzBytesPerUs = 4.9e6;  // stored-dZ form: dZ bytes per time unit (store + reload)
+constexpr double kPlanDzFixedUs = 5.0;
 
 // VALU instructions per element of the activation plane (dX role: act'; dW role: act and act')
 double valu_dx(int act) { return act == ACT_SILU ? 8.5 : act == ACT_SIGMOID ? 6.5 : act == ACT_LEAKY ? 3.0 : 1.0; }
@@ -772,7 +973,8 @@ long long rows_for_split(long long B, long long ns) {
   return rps < DW_BT ? (long long)DW_BT : rps;
 }
 
-BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int num_cus, size_t max_ws) {
+BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int dz_mode, int num_cus,
+                  size_t max_ws) {
   BwdPlan p{};
   p.nE = (int)((E + DW_ET - 1) / DW_ET);
   const long long base = H * (long long)p.nE, N = num_cus > 0 ? num_cus : 1;
@@ -811,22 +1013,64 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
       }
     }
   }
+  // Stored-dZ form: the dW launch alone (programs dealt over the CUs) and its reduction, then
+  // storing dZ and streaming it back through the dX GEMM (memory-bound: a rate per byte, in the
+  // same time units, and a fixed part for the extra launch). Fitted to the same-box times of
+  // cfg2-cfg5 in both forms. FMLP_BWD_DZ (read once per process): 0 never, 1 whenever the
+  // workspace allows it, unset: when the estimate is lower (dz_mode overrides it, per call).
+  static const int dz_env = env_int("FMLP_BWD_DZ", -1);
+  const int dz_want = dz_mode != DZ_AUTO ? (dz_mode == DZ_FORCE ? 1 : 0) : dz_env;
+  const long long Bp = (B + DX2_ROWS - 1) / DX2_ROWS * DX2_ROWS;
+  const size_t dz_head = (size_t)p.nE * DW_ET * (size_t)Bp * 2u;
+  double best_dz = 0.0;
+  long long best_dz_ns = 1;
+  if (dz_want != 0 && B > 0 && dz_head < ((size_t)1 << 31)) {
+    const double t_dx = kPlanDzFixedUs + (double)H * dz_head / kPlanDzBytesPerUs;
+    for (long long ns = 1; ns <= (ns_env > 0 ? 1 : cap); ns *= 2) {
+      const long long want = ns_env > 0 ? (ns_env < max_ns ? ns_env : max_ns) : ns;
+      const long long rps = rows_for_split(B, want), eff = B > rps ? (B + rps - 1) / rps : 1;
+      const size_t need = (ws_for(eff) + 255) / 256 * 256 + (size_t)H * dz_head;
+      if (need > max_ws) break;
+      const double tw = kPlanFixedUs + (double)rps * w_per_row;
+      const double red = eff > 1 ? kPlanLaunchUs + (double)(2 * eff + 1) * H * E * D * 4.0 / kPlanHbmBytesPerUs : 0.0;
+      const double t = list_makespan(base * eff, tw, 0, 0.0, N) + red + t_dx;
+      if (best_dz == 0.0 || t < best_dz) {
+        best_dz = t;
+        best_dz_ns = eff;
+      }
+    }
+  }
+  p.dz = best_dz > 0.0 && (dz_want == 1 || best_dz < best_t);
+  if (p.dz) {
+    best_ns = best_dz_ns;
+    best_dx_first = false;
+  }
   const long long rps = rows_for_split(B, best_ns);
   p.nS = (int)(B > rps ? (B + rps - 1) / rps : 1);
   p.rows_per_split = (int)rps;
   p.n_dw = base * p.nS;
   p.dx_first = best_dx_first;
   p.ws_bytes = ws_for(p.nS);
+  if (p.dz) {
+    p.Bp = (int)Bp;
+    p.dz_off = (p.ws_bytes + 255) / 256 * 256;
+    p.ws_bytes = p.dz_off + (size_t)H * dz_head;
+    p.n_dx = H * (Bp / DX2_ROWS);
+    // dxg_kernel is persistent: one workgroup per CU (a multiple of 8, the XCD count), at most
+    // one per tile
+    p.n_xg = (int)std::min<long long>(p.n_dx, std::max<long long>(8, N / 8 * 8));
+  }
   return p;
 }
 
 }  // namespace
 
 // Plans are computed once per distinct call shape (a small cache of recent ones).
-BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int num_cus, size_t max_ws) {
+BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int dz_mode, int num_cus,
+                 size_t max_ws) {
   struct Entry {
     int64_t H, B, D, E;
-    int act, hilo, cus;
+    int act, hilo, dz, cus;
     size_t max_ws;
     BwdPlan plan;
   };
@@ -837,14 +1081,14 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo,
     std::lock_guard<std::mutex> lock(mu);
     for (int i = 0; i < used; ++i) {
       const Entry& c = cache[i];
-      if (c.H == H && c.B == B && c.D == D && c.E == E && c.act == act && c.hilo == (int)hilo && c.cus == num_cus &&
-          c.max_ws == max_ws)
+      if (c.H == H && c.B == B && c.D == D && c.E == E && c.act == act && c.hilo == (int)hilo &&
+          c.dz == dz_mode && c.cus == num_cus && c.max_ws == max_ws)
         return c.plan;
     }
   }
-  const BwdPlan p = make_plan(H, B, D, E, act, hilo, num_cus, max_ws);
+  const BwdPlan p = make_plan(H, B, D, E, act, hilo, dz_mode, num_cus, max_ws);
   std::lock_guard<std::mutex> lock(mu);
-  cache[next] = Entry{H, B, D, E, act, (int)hilo, num_cus, max_ws, p};
+  cache[next] = Entry{H, B, D, E, act, (int)hilo, dz_mode, num_cus, max_ws, p};
   next = (next + 1) % 16;
   if (used < 16) ++used;
   return p;
@@ -864,6 +1108,29 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
                        a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
     return hipGetLastError();
   };
+  if (p.dz) {  // stored-dZ form: dW programs storing dZ, their reduction, then the dX GEMM
+    u16* dzt = (u16*)((char*)a.ws + p.dz_off);
+    const int Ep = p.nE * DW_ET;
+    auto launch_w = [&](auto k) {
+      static std::atomic<unsigned long long> lds_set{0};
+      hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
+      if (r != hipSuccess) return r;
+      hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
+                         (const u16*)a.w2, (const u16*)a.dout, a.dw1, a.dw2, (float*)a.ws, (int)a.H, (int)a.B,
+                         (int)a.E, p.nE, p.nS, p.rows_per_split, a.out_f32 ? 1 : 0, dzt, p.Bp);
+      return hipGetLastError();
+    };
+    e = a.dw_hilo ? launch_w(dw2_kernel<BF16, D, ACT, true, true>) : launch_w(dw2_kernel<BF16, D, ACT, false, true>);
+    if (e != hipSuccess) return e;
+    if ((e = reduce()) != hipSuccess) return e;
+    const size_t lds_g = (size_t)DXG_ZS * (32 * 256 * 2) + (size_t)DXG_WS * 64 * D;
+    auto kg = dxg_kernel<BF16, D>;
+    static std::atomic<unsigned long long> lds_g_set{0};
+    if ((e = set_lds_once((const void*)kg, (int)lds_g, lds_g_set)) != hipSuccess) return e;
+    hipLaunchKernelGGL(kg, dim3((unsigned)p.n_xg), dim3(DX2_NT), lds_g, st, (const u16*)dzt, (const u16*)a.w1, a.dx,
+                       (int)a.B, p.Bp, (int)a.E, Ep, p.Bp / DX2_ROWS, (int)p.n_dx, a.out_f32 ? 1 : 0);
+    return hipGetLastError();
+  }
   // FMLP_BWD_UNIFIED (read once per process): 1 (default) = one launch holding both roles,
   // 0 = dW programs (and their reduction), then dX programs, as separate launches
   static const int unified = env_int("FMLP_BWD_UNIFIED", 1);
@@ -889,15 +1156,15 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
       if (r != hipSuccess) return r;
       hipLaunchKernelGGL(k, dim3((unsigned)p.n_dw), dim3(DW2_NT), lds, st, (const u16*)a.x, (const u16*)a.w1,
                          (const u16*)a.w2, (const u16*)a.dout, a.dw1, a.dw2, (float*)a.ws, (int)a.H,
-                         (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, a.out_f32 ? 1 : 0);
+                         (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, a.out_f32 ? 1 : 0, (u16*)nullptr, 0);
       return hipGetLastError();
     };
-    e = a.dw_hilo ? launch_w(dw2_kernel<BF16, D, ACT, true>) : launch_w(dw2_kernel<BF16, D, ACT, false>);
+    e = a.dw_hilo ? launch_w(dw2_kernel<BF16, D, ACT, true, false>) : launch_w(dw2_kernel<BF16, D, ACT, false, false>);
     if (e != hipSuccess) return e;
     if ((e = reduce()) != hipSuccess) return e;
   }
   if (p.n_dx > 0) {
-    const size_t lds_x = 4u * 128u * D;  // four chunk slots
+    const size_t lds_x = (size_t)DX_NSLOT * 128u * D;  // the chunk ring
     auto k = dx2_kernel<BF16, D, ACT>;
     static std::atomic<unsigned long long> lds_set{0};
     e = set_lds_once((const void*)k, (int)lds_x, lds_set);

@@ -32,6 +32,8 @@ struct FwdArgs {
 //                rows_per_split rows (nS > 1 writes fp32 partials to the workspace).
 //   dX programs: H * dx_tiles_per_head, each owning 256 rows.
 //   Both 8 waves (two per SIMD), in one launch (bwd_kernel), the longer role first.
+//   Stored-dZ form (dz): the dW programs also store dZ to the workspace and dX is a GEMM over
+//   it (dxg_kernel), two launches instead of recomputing Z and dH in dX programs.
 struct BwdPlan {
   int nE;              // E-tiles of 128 per head
   int nS;              // B splits for the dW programs
@@ -39,7 +41,11 @@ struct BwdPlan {
   int dx_tiles_per_head;
   bool dx_first;       // single-launch order: dX programs before the dW programs
   long long n_dw, n_dx;
-  size_t ws_bytes;     // fp32 partials when nS > 1
+  bool dz;             // stored-dZ form
+  int Bp;              // B rounded up to 256 (dZ tiles), stored-dZ form
+  int n_xg;            // dxg_kernel workgroups (persistent), stored-dZ form
+  size_t dz_off;       // byte offset of dZ in the workspace, stored-dZ form
+  size_t ws_bytes;     // fp32 partials when nS > 1, then dZ (H nE 128 Bp io elements) when dz
 };
 
 struct BwdArgs {
@@ -83,9 +89,11 @@ hipError_t launch_gen_fwd(const GenArgs& a, hipStream_t st);
 hipError_t launch_gen_bwd(const GenArgs& a, hipStream_t st);
 bool gen_supports_d(int64_t D);
 
-// act: activation code; hilo: FMLP_DW_HILO; max_ws: the largest workspace the caller can provide
-// (fmlp_bwd_noalloc: its static scratch)
-BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int num_cus,
+// act: activation code; hilo: FMLP_DW_HILO; dz_mode: whether the stored-dZ form may be chosen
+// (DZ_NEVER: FMLP_BWD_RECOMPUTE, DZ_FORCE: FMLP_BWD_STORE_DZ, whenever the workspace allows);
+// max_ws: the largest workspace the caller can provide (fmlp_bwd_noalloc: its static scratch)
+enum { DZ_NEVER = 0, DZ_AUTO = 1, DZ_FORCE = 2 };
+BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int dz_mode, int num_cus,
                  size_t max_ws = (size_t)-1);
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t st);
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st);

@@ -120,12 +120,16 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
 
 
 def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.Tensor,
-                 activation: str = "", *, accurate_dw: bool = False) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                 activation: str = "", *, accurate_dw: bool = False,
+                 recompute: bool = False) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """FlashMLP backward pass (reference: flashmlp.py:480-538).
 
     Recomputes Z = x @ w1 and h = act(Z) instead of reading stored activations.
-    Returns (dx, dw1, dw2) shaped like (x, w1, w2). accurate_dw=True (no counterpart in the
-    reference) takes h and dZ into the dW products as hi + lo io-dtype terms.
+    Returns (dx, dw1, dw2) shaped like (x, w1, w2). For large shapes the library stores dZ in
+    a temporary workspace (H x ceil(E/128)*128 x ceil(B/256)*256 io elements) and computes dx
+    from it; recompute=True keeps the reference's recompute-only form, whose extra memory is
+    at most the fp32 dW partials. accurate_dw=True takes h and dZ into the dW products as
+    hi + lo io-dtype terms. Both keywords have no counterpart in the reference.
     """
     assert x.shape[0] == w1.shape[0], "Number of heads must match"
     assert x.shape[0] == w2.shape[0], "Number of heads must match"
@@ -138,7 +142,7 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     E = w1.shape[2]
 
     dtype = _check_tensors(x, w1, w2, do)
-    flags = dtype | (_lib.FMLP_DW_HILO if accurate_dw else 0)
+    flags = dtype | (_lib.FMLP_DW_HILO if accurate_dw else 0) | (_lib.FMLP_BWD_RECOMPUTE if recompute else 0)
     dx = torch.empty((H, B, D), dtype=x.dtype, device=x.device)
     dw1 = torch.empty((H, D, E), dtype=x.dtype, device=x.device)
     dw2 = torch.empty((H, E, D), dtype=x.dtype, device=x.device)

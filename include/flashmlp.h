@@ -59,6 +59,20 @@ typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1, FMLP_DTYPE_F32 = 2 } fml
  * the dW programs (8u -> 12u executed FLOPs, u = H B D E). */
 #define FMLP_DW_HILO 0x200
 
+/* OR-ed into the dtype argument of fmlp_bwd / fmlp_bwd_strided / fmlp_bwd_noalloc /
+ * fmlp_bwd_workspace_bytes (rejected by fmlp_fwd): keep the reference's recompute-only
+ * backward (flashmlp.py:341-421), whose workspace is at most the fp32 dW partials of a B split,
+ * instead of the stored-dZ form the library picks for large shapes (see fmlp_bwd). No
+ * counterpart in the reference: for callers that need the backward's memory to stay
+ * O(weights). Results agree with the stored-dZ form within rounding (the same cast points). */
+#define FMLP_BWD_RECOMPUTE 0x400
+
+/* OR-ed into the dtype argument like FMLP_BWD_RECOMPUTE (not together with it): the
+ * stored-dZ form whenever the workspace allows it, whatever the estimate says. A test and
+ * diagnostic flag with no counterpart in the reference (it lets a caller run both forms on
+ * the same shapes). */
+#define FMLP_BWD_STORE_DZ 0x800
+
 /* Activation codes; names as in the reference ("", "silu", "leaky_relu", "sigmoid"). */
 typedef enum { FMLP_ACT_NONE = 0, FMLP_ACT_SILU = 1, FMLP_ACT_LEAKY_RELU = 2, FMLP_ACT_SIGMOID = 3 } fmlp_act;
 
@@ -102,15 +116,21 @@ int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int
                      int64_t E, const int64_t* x_strides, const int64_t* w1_strides, const int64_t* w2_strides,
                      int dtype, int act, void* stream);
 
-/* Bytes of device workspace fmlp_bwd needs for these shapes and dtype flags (FMLP_DW_HILO
- * changes it) on the current device, whatever the activation (0 when none is needed). */
+/* Bytes of device workspace fmlp_bwd needs for these shapes and dtype flags (FMLP_DW_HILO and
+ * FMLP_BWD_RECOMPUTE change it) on the current device, whatever the activation (0 when none is
+ * needed). */
 size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
 /*
  * Backward: dx = dZ @ w1^T, dw1 = x^T @ dZ, dw2 = h^T @ dout with h = act(x @ w1),
- * dZ = (dout @ w2^T) * act'(x @ w1); Z and h are recomputed, never stored. Replaces
- * flashmlp_bwd's kernel launch (flashmlp.py:480-538, kernel flashmlp.py:341-421).
- * dx, dw1, dw2 are fully overwritten. `workspace` may be NULL when
+ * dZ = (dout @ w2^T) * act'(x @ w1); Z and h are recomputed from x, never stored by the forward.
+ * Replaces flashmlp_bwd's kernel launch (flashmlp.py:480-538, kernel flashmlp.py:341-421).
+ * Two forms, chosen per shape by an estimate of their time: the reference's, whose dX programs
+ * recompute Z and dH (one launch), and a stored-dZ form for large shapes, whose dW programs
+ * also write dZ (in the io dtype: the value the dX product takes) to the workspace and dx is a
+ * GEMM over it (two launches, 10u instead of 14u of matrix work, u = H B D E, at
+ * H ceil(E/128) 128 ceil(B/256) 256 io elements of workspace). FMLP_BWD_RECOMPUTE keeps the
+ * first. dx, dw1, dw2 are fully overwritten. `workspace` may be NULL when
  * fmlp_bwd_workspace_bytes() is 0.
  */
 int fmlp_bwd(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1, void* dw2,
@@ -130,10 +150,12 @@ int fmlp_bwd_strided(const void* x, const void* w1, const void* w2, const void* 
  * static device scratch (FMLP_SCRATCH_MAX_BYTES per device, held from the first call on a
  * device until the process ends). No counterpart in the reference: for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). It calls no hipMalloc, hipFree or allocating routine. Shapes whose
- * fmlp_bwd_workspace_bytes() exceeds FMLP_SCRATCH_MAX_BYTES return FMLP_ERR_WORKSPACE. All
- * calls on one device share that device's scratch: calls that overlap on one device (other
- * streams, other threads) race; serialise them.
+ * forbid hipMalloc). It calls no hipMalloc, hipFree or allocating routine. It only takes the
+ * forms whose workspace fits the scratch (the stored-dZ form only when dZ fits); shapes whose
+ * recompute-only workspace (fmlp_bwd_workspace_bytes with FMLP_BWD_RECOMPUTE) exceeds
+ * FMLP_SCRATCH_MAX_BYTES return FMLP_ERR_WORKSPACE. All calls on one device share that
+ * device's scratch: calls that overlap on one device (other streams, other threads) race;
+ * serialise them.
  */
 #define FMLP_SCRATCH_MAX_BYTES ((size_t)64 << 20)
 int fmlp_bwd_noalloc(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1, void* dw2,

@@ -81,7 +81,10 @@ def test_shape_support(L):
     # so is the backward's hi/lo dW flag, alone or with the fp32-output flag; unknown bits are not
     assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_DW_HILO) == 1
     assert L.fmlp_shape_supported(2, 8, 64, 64, 0 | _lib.FMLP_DW_HILO | _lib.FMLP_OUT_F32) == 1
-    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | 0x400) == 0
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_BWD_RECOMPUTE) == 1
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_BWD_STORE_DZ) == 1
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_BWD_STORE_DZ | _lib.FMLP_BWD_RECOMPUTE) == 0
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | 0x1000) == 0
     assert L.fmlp_shape_supported(-1, 8, 64, 64, 1) == 0
 
 
@@ -101,6 +104,8 @@ def _fwd(L, x=0x1000, w1=0x1000, w2=0x1000, o=0x1000, H=2, B=8, D=64, E=64, dtyp
 
 def test_forward_argument_validation(L):
     assert _fwd(L, dtype=1 | _lib.FMLP_DW_HILO) == INVALID  # a backward-only flag
+    assert _fwd(L, dtype=1 | _lib.FMLP_BWD_RECOMPUTE) == INVALID  # a backward-only flag
+    assert _fwd(L, dtype=1 | _lib.FMLP_BWD_STORE_DZ) == INVALID  # a backward-only flag
     assert _fwd(L, D=96) == UNSUPPORTED
     assert b"D=96" in L.fmlp_last_error()
     assert _fwd(L, E=0) == UNSUPPORTED

@@ -37,10 +37,10 @@ def _outs(x, w1):
             torch.empty(H, E, D, dtype=x.dtype, device=x.device))
 
 
-def _bwd_ws(L, x, w1, w2, do, act):
+def _bwd_ws(L, x, w1, w2, do, act, flags=0):
     H, B, D = x.shape
     E = w1.shape[2]
-    code = _DT[x.dtype]
+    code = _DT[x.dtype] | flags
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     n = L.fmlp_bwd_workspace_bytes(H, B, D, E, code)
     ws = torch.empty(max(n, 16), dtype=torch.uint8, device=x.device)
@@ -50,26 +50,28 @@ def _bwd_ws(L, x, w1, w2, do, act):
     return (dx, dw1, dw2), n
 
 
-def _bwd_noalloc(L, x, w1, w2, do, act):
+def _bwd_noalloc(L, x, w1, w2, do, act, flags=0):
     H, B, D = x.shape
     E = w1.shape[2]
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     dx, dw1, dw2 = _outs(x, w1)
     _lib.check(L.fmlp_bwd_noalloc(_p(x), _p(w1), _p(w2), _p(do), _p(dx), _p(dw1), _p(dw2), H, B, D, E,
-                                  _DT[x.dtype], _lib.ACT_CODES[act], stream), "backward (no allocation)")
+                                  _DT[x.dtype] | flags, _lib.ACT_CODES[act], stream), "backward (no allocation)")
     return dx, dw1, dw2
 
 
 def test_noalloc_matches_workspace_entry_point_twice():
     L = _lib.lib()
-    # first: the cfg3 shape (B split 2 ways, 16.8 MB of partials); second: smaller
-    cases = [(16, 8192, 128, 512, torch.bfloat16, "leaky_relu", 21), (6, 1500, 64, 264, torch.float16, "silu", 22)]
-    for H, B, D, E, dt, act, seed in cases:
-        _say(f"[noalloc] H={H} B={B} D={D} E={E} {dt} act='{act}' seed={seed}")
+    # first: the cfg3 shape in the recompute-only form (B split, 16.8 MB or more of partials);
+    # second: smaller, whatever form the plan picks (its workspace fits the scratch either way)
+    cases = [(16, 8192, 128, 512, torch.bfloat16, "leaky_relu", 21, _lib.FMLP_BWD_RECOMPUTE),
+             (6, 1500, 64, 264, torch.float16, "silu", 22, 0)]
+    for H, B, D, E, dt, act, seed, flags in cases:
+        _say(f"[noalloc] H={H} B={B} D={D} E={E} {dt} act='{act}' seed={seed} flags={flags:#x}")
         x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=seed))
-        ref, n = _bwd_ws(L, x, w1, w2, do, act)
+        ref, n = _bwd_ws(L, x, w1, w2, do, act, flags)
         assert 0 < n <= _lib.FMLP_SCRATCH_MAX_BYTES, n  # the scratch path is exercised
-        got = _bwd_noalloc(L, x, w1, w2, do, act)
+        got = _bwd_noalloc(L, x, w1, w2, do, act, flags)
         torch.cuda.synchronize()
         for g, r in zip(got, ref):
             g, r = g.float(), r.float()
@@ -84,15 +86,15 @@ def test_noalloc_without_split_and_scratch_bound():
     H, B, D, E = 32, 600, 128, 1024
     x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, torch.bfloat16, seed=23))
     _say(f"[noalloc] no-split H={H} B={B} D={D} E={E}")
-    ref, n = _bwd_ws(L, x, w1, w2, do, "silu")
-    got = _bwd_noalloc(L, x, w1, w2, do, "silu")
+    ref, n = _bwd_ws(L, x, w1, w2, do, "silu", _lib.FMLP_BWD_RECOMPUTE)
+    got = _bwd_noalloc(L, x, w1, w2, do, "silu", _lib.FMLP_BWD_RECOMPUTE)
     torch.cuda.synchronize()
     assert n == 0
     for g, r in zip(got, ref):
         assert torch.equal(g, r)
     # the fp32 partials exist only while H * ceil(E / 128) dW programs leave CUs idle; their
     # size peaks just below one program per CU: at D = 128 every supported shape fits
-    worst = max(L.fmlp_bwd_workspace_bytes(h, 1 << 20, 128, 128 * ne, _lib.FMLP_DTYPE_BF16)
+    worst = max(L.fmlp_bwd_workspace_bytes(h, 1 << 20, 128, 128 * ne, _lib.FMLP_DTYPE_BF16 | _lib.FMLP_BWD_RECOMPUTE)
                 for h in range(1, 300) for ne in (1, 2, 3))
     _say(f"[noalloc] largest partial workspace over H <= 299, E <= 384, D = 128: {worst} bytes")
     assert 0 < worst <= _lib.FMLP_SCRATCH_MAX_BYTES
