@@ -742,14 +742,15 @@ dw_reduce_kernel(const float* __restrict__ ws, void* __restrict__ dW1, void* __r
 // programs store dZ (the io-dtype value the reference's dX product takes,
 // flashmlp.py:227-235) instead of the dX programs recomputing Z and dH. A tile is 256 rows
 // of one head (one contiguous block of dZ, chunk after chunk), 8 waves x 32 rows; per 32-column
-// E-chunk c a wave issues D/16 MFMAs dX += dZ(c) W1c(c)^T.
+// E-chunk c a wave issues D/16 MFMAs dX^T += W1c(c) dZ(c)^T (the transposed product: each lane
+// ends with whole row pieces of dX and stores them 8 or 16 bytes at a time).
 // Persistent: one workgroup per CU walks its tiles as one stream of (tile, chunk) steps, so
 // the loads run ahead across tile boundaries and no tile pays the memory latency up front.
 // LDS: a ring of dZ chunks (8 blocks [32 e][32 positions], 64-byte rows; block w = wave w's
 // rows, read with ds_read_b64_tr_b16 like a row-major [e][b] tile) streamed from HBM 7 steps
 // ahead, and a ring of W1c chunks ([D][32], 64-byte rows, 16-byte chunk q of row r at
 // q ^ ((r >> 2) & 3), read row-wise; L2-resident) 3 steps ahead. One barrier per step.
-// Stored positions are sig-permuted within 16 rows, so C-layout row m is row sig(m).
+// Stored positions are sig-permuted within 16 rows: the lane holding position m holds row sig(m).
 // ------------------------------------------------------------------------------------
 constexpr int DXG_ZS = 8;  // dZ chunk ring slots (16 KB each)
 constexpr int DXG_ZPF = 7; // dZ chunks requested ahead: step j + 7 reuses the slot of step j - 1
@@ -873,33 +874,36 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
 #pragma unroll
       for (int nt = 0; nt < NTN; ++nt) b[s2][nt] = lds_read16(wb + offB[s2] + nt * 2048);
     }
+    // dX^T tile nt = W1c rows 32 nt .. (A) times the dZ positions (B): C layout lane = position
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) acc[nt] = mfma<BF16>(a[s2], b[s2][nt], acc[nt]);
-    if (++c == NC) {  // tile done: store its rows (C layout: lane = column d, position m -> row sig(m))
+      for (int nt = 0; nt < NTN; ++nt) acc[nt] = mfma<BF16>(b[s2][nt], a[s2], acc[nt]);
+    if (++c == NC) {  // tile done: lane l32 holds row sig(l32) of the wave's 32, columns
+                      // 32 nt + 8 q + 4 g + 0..3 in acc[nt][4 q .. 4 q + 3]: 8- or 16-byte stores
       const int t = tile_of(k);  // once per tile
       const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
-      const int b_wave = bt * DX2_ROWS + wave * 32;
-      if (outf32) {
-        float* o = (float*)dX + (size_t)h * B * D;
+      const int b = bt * DX2_ROWS + wave * 32 + (int)sig((unsigned)l32);
+      if (b < B) {
+        if (outf32) {
+          float* o = (float*)dX + ((size_t)h * B + b) * D + 4 * g;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int b = b_wave + (int)sig(8 * (i >> 2) + 4 * g + (i & 3));
-          if (b < B) {
+          for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-            for (int nt = 0; nt < NTN; ++nt) o[(size_t)b * D + nt * 32 + l32] = acc[nt][i];
-          }
-        }
-      } else {
-        u16* o = (u16*)dX + (size_t)h * B * D;
+            for (int q = 0; q < 4; ++q) {
+              const float4 v = {acc[nt][4 * q], acc[nt][4 * q + 1], acc[nt][4 * q + 2], acc[nt][4 * q + 3]};
+              *(float4*)(o + 32 * nt + 8 * q) = v;
+            }
+        } else {
+          u16* o = (u16*)dX + ((size_t)h * B + b) * D + 4 * g;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int b = b_wave + (int)sig(8 * (i >> 2) + 4 * g + (i & 3));
-          if (b < B) {
+          for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-            for (int nt = 0; nt < NTN; ++nt) o[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(acc[nt][i]);
-          }
+            for (int q = 0; q < 4; ++q) {
+              const u32x2 v = {pack2<BF16>(acc[nt][4 * q], acc[nt][4 * q + 1]),
+                               pack2<BF16>(acc[nt][4 * q + 2], acc[nt][4 * q + 3])};
+              *(u32x2*)(o + 32 * nt + 8 * q) = v;
+            }
         }
       }
 #pragma unroll
