@@ -155,6 +155,10 @@ def peak_memory(x, w1, w2, do, activation):
         o = fm.flashmlp_fwd(x, w1, w2, activation)
         return o, (lambda: fm.flashmlp_bwd(x, w1, w2, do, activation))
 
+    def flash_recompute():  # the recompute-only backward (no stored dZ)
+        o = fm.flashmlp_fwd(x, w1, w2, activation)
+        return o, (lambda: fm.flashmlp_bwd(x, w1, w2, do, activation, recompute=True))
+
     def unfused():
         z = torch.bmm(x, w1)
         h = {"silu": torch.nn.functional.silu, "sigmoid": torch.sigmoid,
@@ -180,7 +184,7 @@ def peak_memory(x, w1, w2, do, activation):
         return o, bwd
 
     out = {}
-    for name, fn in (("flashmlp", flash), ("pytorch_unfused", unfused)):
+    for name, fn in (("flashmlp", flash), ("flashmlp_recompute", flash_recompute), ("pytorch_unfused", unfused)):
         o, b = fn()
         b()
         del o, b
@@ -197,6 +201,7 @@ def peak_memory(x, w1, w2, do, activation):
         torch.cuda.empty_cache()
         out[name] = {"fwd_alloc_mb": round(fwd_mb, 1), "peak_mb": round(peak_mb, 1)}
     out["peak_savings"] = round(1 - out["flashmlp"]["peak_mb"] / out["pytorch_unfused"]["peak_mb"], 4)
+    out["peak_savings_recompute"] = round(1 - out["flashmlp_recompute"]["peak_mb"] / out["pytorch_unfused"]["peak_mb"], 4)
     return out
 
 
@@ -461,9 +466,17 @@ def main():
         line["bwd_ms"] = round(bwd_ms, 4)
         line["bwd_tflops"] = round(bwd_tf, 2)
         line["bwd_hbm_gbs"] = round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1)
+        from flashmlp_amd import _lib
+        code = (_lib.FMLP_DTYPE_BF16 if dt_name == "bf16" else _lib.FMLP_DTYPE_F16) | \
+            (_lib.FMLP_DW_HILO if args.accurate_dw else 0)
+        stores_dz = bool(_lib.lib().fmlp_bwd_stores_dz(H, B, D, E, code, _lib.ACT_CODES[act]))
+        line["bwd_form"] = "stored-dZ" if stores_dz else "recompute"
         line["roofline"] = {
-            "kernel": "fmlp_bwd call: fmlp::bwd_kernel (dW and dX programs in one launch; then"
-                      " fmlp::dw_reduce_kernel when the dW programs split B)",
+            "kernel": ("fmlp_bwd call, stored-dZ form: fmlp::dw2_kernel (dW programs, also writing dZ), "
+                       "fmlp::dw_reduce_kernel when they split B, then fmlp::dxg_kernel (dX = dZ W1^T)"
+                       if stores_dz else
+                       "fmlp_bwd call, recompute form: fmlp::bwd_kernel (dW and dX programs in one launch; "
+                       "then fmlp::dw_reduce_kernel when the dW programs split B)"),
             "bound": "mfma",
             "achieved": round(bwd_tf, 2),
             "peak": peak,

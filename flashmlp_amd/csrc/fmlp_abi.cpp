@@ -278,6 +278,14 @@ FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int
   return n;
 }
 
+FMLP_EXPORT int fmlp_bwd_stores_dz(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act) {
+  if (check_shape(H, B, D, E, dtype) != FMLP_OK || check_act(act) != FMLP_OK) return 0;
+  if (!tuned_shape(D, E, io_of(dtype))) return 0;  // the generic kernels recompute
+  int cus = 0;
+  if (num_cus_current(&cus) != FMLP_OK) return 0;
+  return fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus).dz ? 1 : 0;
+}
+
 namespace {
 
 // The backward of every entry point: argument checks, then the tuned kernels (dense, aligned,

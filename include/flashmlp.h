@@ -121,6 +121,11 @@ int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int
  * needed). */
 size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
+/* 1 when fmlp_bwd takes the stored-dZ form for these shapes, dtype flags and activation on the
+ * current device, else 0 (also for rejected arguments). No counterpart in the reference: for
+ * callers planning memory and for benches naming the kernels they time. */
+int fmlp_bwd_stores_dz(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act);
+
 /*
  * Backward: dx = dZ @ w1^T, dw1 = x^T @ dZ, dw2 = h^T @ dout with h = act(x @ w1),
  * dZ = (dout @ w2^T) * act'(x @ w1); Z and h are recomputed from x, never stored by the forward.

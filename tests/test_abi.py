@@ -153,6 +153,11 @@ def test_backward_argument_validation(L):
 
 def test_workspace_query_is_zero_for_invalid_shapes(L):
     assert L.fmlp_bwd_workspace_bytes(2, 8, 96, 64, 1) == 0
+    # the backward-form query answers 0 for rejected arguments (and for the generic kernels)
+    assert L.fmlp_bwd_stores_dz(2, 8, 96, 64, 1, 1) == 0
+    assert L.fmlp_bwd_stores_dz(2, 8, 64, 64, 1, -1) == 0
+    assert L.fmlp_bwd_stores_dz(2, 8, 64, 64, 1 | _lib.FMLP_BWD_RECOMPUTE | _lib.FMLP_BWD_STORE_DZ, 1) == 0
+    assert L.fmlp_bwd_stores_dz(2, 8, 64, 64, _lib.FMLP_DTYPE_F32, 1) == 0
 
 
 def test_last_error_is_thread_local(L):
