@@ -743,7 +743,7 @@ dw_reduce_kernel(const float* __restrict__ ws, void* __restrict__ dW1, void* __r
 // flashmlp.py:227-235) instead of the dX programs recomputing Z and dH. A tile is 256 rows
 // of one head (one contiguous block of dZ, chunk after chunk), 8 waves x 32 rows; per 32-column
 // E-chunk c a wave issues D/16 MFMAs dX^T += W1c(c) dZ(c)^T (the transposed product: each lane
-// ends with whole row pieces of dX and stores them 8 or 16 bytes at a time).
+// ends with whole row pieces of dX; a lane swap makes each bf16/fp16 store 16 bytes).
 // Persistent: one workgroup per CU walks its tiles as one stream of (tile, chunk) steps, so
 // the loads run ahead across tile boundaries and no tile pays the memory latency up front.
 // LDS: a ring of dZ chunks (8 blocks [32 e][32 positions], 64-byte rows; block w = wave w's
@@ -856,8 +856,18 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
     }
   }
   int c = 0, k = 0;  // chunk and tile of step j
+  int since = 1 << 20;  // steps since the last tile end
   for (int j = 0; j < steps; ++j) {
-    wait_vmcnt<(NZ + 1) * (DXG_WPF - 1)>();  // this wave's pieces of step j (dZ and W1c)
+    // this wave's pieces of step j (dZ and W1c) have landed: the loads of steps j - 2, j - 1 may
+    // stay in flight and, when a tile ended in steps j - 3 .. j - 1 (one at most when NC >= 3),
+    // that tile's stores, issued after W1c(j) (vmcnt counts loads and stores in issue order)
+    constexpr int NW0 = (NZ + 1) * (DXG_WPF - 1);
+    if (++since <= DXG_WPF && NC >= DXG_WPF) {
+      if (outf32) wait_vmcnt<NW0 + 4 * NTN>();
+      else wait_vmcnt<NW0 + 2 * NTN>();
+    } else {
+      wait_vmcnt<NW0>();
+    }
     __builtin_amdgcn_s_waitcnt(0xC07F);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();  // step j visible; step j - 1 no longer read
@@ -880,32 +890,42 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
 #pragma unroll
       for (int nt = 0; nt < NTN; ++nt) acc[nt] = mfma<BF16>(b[s2][nt], a[s2], acc[nt]);
     if (++c == NC) {  // tile done: lane l32 holds row sig(l32) of the wave's 32, columns
-                      // 32 nt + 8 q + 4 g + 0..3 in acc[nt][4 q .. 4 q + 3]: 8- or 16-byte stores
+                      // 32 nt + 8 q + 4 g + 0..3 in acc[nt][4 q .. 4 q + 3]: 16-byte buffer
+                      // stores, rows past B out of range
       const int t = tile_of(k);  // once per tile
       const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
-      const int b = bt * DX2_ROWS + wave * 32 + (int)sig((unsigned)l32);
-      if (b < B) {
-        if (outf32) {
-          float* o = (float*)dX + ((size_t)h * B + b) * D + 4 * g;
+      const int rows = clamp0(B - bt * DX2_ROWS, DX2_ROWS);
+      const unsigned r = (unsigned)(wave * 32) + sig((unsigned)l32);
+      if (outf32) {
+        const Rsrc ro = make_rsrc((const float*)dX + ((size_t)h * B + (size_t)bt * DX2_ROWS) * D, rows * D * 4);
 #pragma unroll
-          for (int nt = 0; nt < NTN; ++nt)
+        for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const float4 v = {acc[nt][4 * q], acc[nt][4 * q + 1], acc[nt][4 * q + 2], acc[nt][4 * q + 3]};
-              *(float4*)(o + 32 * nt + 8 * q) = v;
-            }
-        } else {
-          u16* o = (u16*)dX + ((size_t)h * B + b) * D + 4 * g;
+          for (int q = 0; q < 4; ++q) {
+            const u32x4 v = {__float_as_uint(acc[nt][4 * q]), __float_as_uint(acc[nt][4 * q + 1]),
+                             __float_as_uint(acc[nt][4 * q + 2]), __float_as_uint(acc[nt][4 * q + 3])};
+            __builtin_amdgcn_raw_buffer_store_b128(v, ro, (int)((r * D + 32 * nt + 8 * q + 4 * g) * 4u), 0, 0);
+          }
+      } else {
+        const Rsrc ro = make_rsrc((const u16*)dX + ((size_t)h * B + (size_t)bt * DX2_ROWS) * D, rows * D * 2);
 #pragma unroll
-          for (int nt = 0; nt < NTN; ++nt)
+        for (int nt = 0; nt < NTN; ++nt) {
+          u32x2 v[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const u32x2 v = {pack2<BF16>(acc[nt][4 * q], acc[nt][4 * q + 1]),
-                               pack2<BF16>(acc[nt][4 * q + 2], acc[nt][4 * q + 3])};
-              *(u32x2*)(o + 32 * nt + 8 * q) = v;
-            }
+          for (int q = 0; q < 4; ++q)
+            v[q] = u32x2{pack2<BF16>(acc[nt][4 * q], acc[nt][4 * q + 1]), pack2<BF16>(acc[nt][4 * q + 2], acc[nt][4 * q + 3])};
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            // lanes 0-31 hold columns 8q + 0..3, lanes 32-63 8q + 4..7: one swap gives lane g
+            // columns 16 p + 8 g .. + 7
+            const auto s0 = __builtin_amdgcn_permlane32_swap(v[2 * p][0], v[2 * p + 1][0], false, false);
+            const auto s1 = __builtin_amdgcn_permlane32_swap(v[2 * p][1], v[2 * p + 1][1], false, false);
+            const u32x4 w = {s0[0], s1[0], s0[1], s1[1]};
+            __builtin_amdgcn_raw_buffer_store_b128(w, ro, (int)((r * D + 32 * nt + 16 * p + 8 * g) * 2u), 0, 0);
+          }
         }
       }
+      since = 0;
 #pragma unroll
       for (int nt = 0; nt < NTN; ++nt) acc[nt] = zero16();
       c = 0;
