@@ -777,9 +777,18 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
   const int nwg = (int)gridDim.x, wg = (int)blockIdx.x;
   const int my_tiles = wg < n_tiles ? (n_tiles - 1 - wg) / nwg + 1 : 0;
   const int steps = my_tiles * NC;
-  // tile k of this workgroup: virtual index k * nwg + wg (dispatch order: XCD = index % 8, as
-  // nwg is a multiple of 8), remapped so each XCD walks a contiguous range of tiles (heads)
-  auto tile_of = [&](int k) { return xcd_remap(k * nwg + wg, n_tiles); };
+  // tile k of this workgroup: virtual index v = k * nwg + wg, taken in descending row order over
+  // all heads (v = 0 .. H - 1 are the last 256-row tiles of heads 0 .. H - 1). The dW programs
+  // walk their rows upwards, so the dZ they stored last is read first, while the device's
+  // memory-side cache still holds it (measured at cfg4: 288 -> 270 us). When nwg is a multiple
+  // of H (cfg4: 256 and 32), workgroup wg serves head wg mod H only, on XCD wg mod 8 (the
+  // dispatch order), so each XCD's L2 holds the W1 of H / 8 heads.
+  const int n_heads = n_tiles / tiles_per_head;
+  auto tile_of = [&](int k) {
+    const int v = k * nwg + wg;
+    const int h = v % n_heads, bt = tiles_per_head - 1 - v / n_heads;
+    return h * tiles_per_head + bt;
+  };
 
   // dZ piece p = k * 512 + 64 wave + lane: the chunk is stored as its LDS image, 16 p either way
   unsigned zOff[NZ];
