@@ -231,7 +231,9 @@ int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, 
   const bool dense = sx == nullptr || (is_dense3(sx, B, D) && is_dense3(sw1, D, E) && is_dense3(sw2, E, D));
   hipError_t e;
   if (dense && tuned_shape(D, E, io) && aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(o)) {
-    fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, io == FMLP_DTYPE_BF16, act, (dtype & FMLP_OUT_F32) != 0};
+    int cus = 0;
+    if ((st = num_cus_current(&cus))) return st;
+    fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, io == FMLP_DTYPE_BF16, act, (dtype & FMLP_OUT_F32) != 0, cus};
     e = fmlp::launch_fwd(a, (hipStream_t)stream);
   } else {
     fmlp::GenArgs g = gen_args(x, w1, w2, nullptr, o, nullptr, nullptr, nullptr, H, B, D, E, dtype, act);

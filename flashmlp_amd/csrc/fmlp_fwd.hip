@@ -30,19 +30,24 @@ namespace fmlp {
 //   W2c  [D/32][32][32]    block nt, row e = W2[h][32c + e][32nt .. 32nt+31]
 // Waves per workgroup: one 32-row M-tile each, so that the workgroup's threads cover a chunk's
 // 4 D pieces of W1c and of W2c exactly once (NT == 4 D); two waves per SIMD either way.
+// ES = 2 (E split, D = 64 only, for grids that leave CUs idle): the workgroup holds two such
+// sets of waves on the same rows, each walking half of the E-chunks through a ring of its own
+// (one workgroup per CU, two waves per SIMD instead of one); the two partial O tiles are added
+// through LDS at the end.
 __host__ __device__ constexpr int fwd_waves(int D) { return D / 16; }
 constexpr int FWD_NSLOT = 8;  // LDS ring slots (chunks)
 constexpr int FWD_PF = 4;     // chunks loaded ahead (with one barrier per chunk)
 constexpr int FWD_SB = 2;     // chunk iterations per workgroup barrier
 
-template <bool BF16, int D, int ACT>
-__global__ void __launch_bounds__(fwd_waves(D) * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+template <bool BF16, int D, int ACT, int ES>
+__global__ void __launch_bounds__(fwd_waves(D) * ES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            void* __restrict__ O, int B, int E, int tiles_per_head, int outf32) {
-  constexpr int NW = fwd_waves(D), NT = NW * 64;  // waves, threads
+  constexpr int NW = fwd_waves(D), NT = NW * 64;  // waves, threads of one E part
   constexpr int KS = D / 16;           // K steps of GEMM1 (= GEMM2 operand count 2 * D/32)
   constexpr int NTN = D / 32;          // N tiles of GEMM2
   constexpr int BB = NW * 32;          // rows per workgroup (32 per wave)
+  static_assert(ES == 1 || (ES == 2 && D == 64), "E split");
   constexpr unsigned SLOT = 128u * D;  // bytes per ring slot: W1c (64*D) + W2c (64*D)
   constexpr unsigned W2OFF = 64u * D;
   // SB: chunk iterations per workgroup barrier. The loads run SB - 1 chunks further ahead so
@@ -53,11 +58,17 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   static_assert(SB == 1 || SB == 2, "barrier spacing");
   static_assert(PF >= 2 && PF <= NSLOT - 2 - (SB - 1) && (NSLOT & (NSLOT - 1)) == 0, "ring");
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63;
+  const int part = ES == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x / NT);  // E part
+  const int tid = threadIdx.x - part * NT, wave = tid >> 6;  // thread and wave within the part
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
   const int t = xcd_remap(blockIdx.x, gridDim.x);
   const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
-  const int NC = (E + 31) >> 5;
+  // chunks of this part: global chunk c0 + c for c = 0 .. NC - 1 (the last part's last chunks
+  // may lie past E: they load as zeros and add nothing)
+  const int NC = (((E + 31) >> 5) + ES - 1) / ES;
+  const int c0 = part * NC;
+  const unsigned RB = (unsigned)part * FWD_NSLOT * 128u * D;  // this part's ring
 
   const u16* Xh = X + (size_t)h * B * D;
   const u16* W1h = W1 + (size_t)h * D * E;
@@ -74,11 +85,12 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const unsigned dOffW1 = (unsigned)(tid >> 2) * (unsigned)E * 2u + (tid & 3u) * 16u;
   const unsigned dOffW2 = ((tid >> 2) & 31u) * (D * 2u) + (unsigned)(tid >> 7) * 64u + (tid & 3u) * 16u;
   auto dma_chunk = [&](int c) {
-    const int lim = E - c * 32;
-    const int rem = D * E * 2 - 64 * c;
-    const i32x4 r1 = make_rsrc_words(W1h + (size_t)c * 32, rem > 0 ? rem : 0);
-    const i32x4 r2 = make_rsrc_words(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
-    const int slot = (c & (NSLOT - 1)) * (int)SLOT + wave * 1024;
+    const int cg = c0 + c;
+    const int lim = E - cg * 32;
+    const int rem = D * E * 2 - 64 * cg;
+    const i32x4 r1 = make_rsrc_words(W1h + (size_t)cg * 32, rem > 0 ? rem : 0);
+    const i32x4 r2 = make_rsrc_words(W2h + (size_t)cg * 32 * D, clamp0(lim, 32) * D * 2);
+    const int slot = (int)RB + (c & (NSLOT - 1)) * (int)SLOT + wave * 1024;
     buf_load16_lds(r1, colq < lim ? dOffW1 : BUF_OOB, slot);
     buf_load16_lds(r2, dOffW2, slot + (int)W2OFF);
   };
@@ -140,7 +152,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   St sa, sb;
   sa.z = zero16();
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) sa.z = mfma<BF16>(opndA(0, ks), xr[ks], sa.z);
+  for (int ks = 0; ks < KS; ++ks) sa.z = mfma<BF16>(opndA(RB, ks), xr[ks], sa.z);
 
   // Iteration c (G1: Z^T(c+1) = W1c(c+1)^T X^T, G2: O += h(c-1) W2c(c-1), act: h(c)), reading
   // `in` (Z^T(c), h(c-1)) and writing `out` (Z^T(c+1), h(c)). Written as a fixed sequence of
@@ -151,7 +163,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     constexpr bool DO_G2 = decltype(G2)::value;
     constexpr int N1 = DO_G1 ? KS : 0, N2 = DO_G2 ? KS : 0, NOPS = N1 + N2;
     constexpr int PER = 16 / NOPS;  // activation elements per step
-    const unsigned base1 = ((c + 1) & (NSLOT - 1)) * SLOT, base2 = ((c - 1) & (NSLOT - 1)) * SLOT;
+    const unsigned base1 = RB + ((c + 1) & (NSLOT - 1)) * SLOT, base2 = RB + ((c - 1) & (NSLOT - 1)) * SLOT;
 
     // chunk c+PF is requested straight into its LDS slot (PF chunks ahead of the one read)
     dma_chunk(c + PF);
@@ -195,7 +207,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     if constexpr (decltype(SYNC)::value) chunk_end();
   };
   auto last_gemm2 = [&](const St& st) {
-    const unsigned base2 = ((NC - 1) & (NSLOT - 1)) * SLOT;
+    const unsigned base2 = RB + ((NC - 1) & (NSLOT - 1)) * SLOT;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -232,6 +244,30 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   }
 
   wait_vmcnt<0>();  // chunks past the last are still landing (as zeros)
+  if constexpr (ES == 2) {  // part 1 hands its partial O tile to part 0 through LDS (the rings)
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    const int ob = wave * (NTN * 4096);  // per wave NTN x 4 x [64 lanes][16 bytes]
+    if (part == 1) {
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4)
+          lds_write16(ob + ((nt * 4 + i4) * 64 + lane) * 16,
+                      u32x4{__float_as_uint(o[nt][4 * i4]), __float_as_uint(o[nt][4 * i4 + 1]),
+                            __float_as_uint(o[nt][4 * i4 + 2]), __float_as_uint(o[nt][4 * i4 + 3])});
+    }
+    __syncthreads();
+    if (part == 1) return;
+#pragma unroll
+    for (int nt = 0; nt < NTN; ++nt)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const u32x4 v = lds_read16(ob + ((nt * 4 + i4) * 64 + lane) * 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[nt][4 * i4 + j] += __uint_as_float(v[j]);
+      }
+  }
   // ---- epilogue: O tile (C layout: lane = column d, rows 8(i/4) + 4g + i%4); fp32 sums
   // when the caller asked for them (FMLP_OUT_F32), else rounded to the io dtype ----
   if (outf32) {
@@ -260,6 +296,19 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 // ------------------------------------------------------------------------------------
 // launcher
 // ------------------------------------------------------------------------------------
+template <bool BF16, int D, int ACT, int ES>
+static hipError_t launch_fwd_e(const FwdArgs& a, int tiles_per_head, long long grid, hipStream_t st) {
+  const size_t lds = (size_t)ES * FWD_NSLOT * 128u * D;
+  auto k = fwd_kernel<BF16, D, ACT, ES>;
+  static std::atomic<unsigned long long> lds_set{0};
+  hipError_t e = set_lds_once((const void*)k, (int)lds, lds_set);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(64 * ES * fwd_waves(D)), lds, st, (const u16*)a.x,
+                     (const u16*)a.w1, (const u16*)a.w2, a.o, (int)a.B, (int)a.E, tiles_per_head,
+                     a.out_f32 ? 1 : 0);
+  return hipGetLastError();
+}
+
 template <bool BF16, int D, int ACT>
 static hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   constexpr int BB = 32 * fwd_waves(D);
@@ -267,14 +316,15 @@ static hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   const long long grid = (long long)tiles_per_head * a.H;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
-  const size_t lds = (size_t)FWD_NSLOT * 128u * D;
-  auto k = fwd_kernel<BF16, D, ACT>;
-  static std::atomic<unsigned long long> lds_set{0};
-  hipError_t e = set_lds_once((const void*)k, (int)lds, lds_set);
-  if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(64 * fwd_waves(D)), lds, st, (const u16*)a.x, (const u16*)a.w1,
-                     (const u16*)a.w2, a.o, (int)a.B, (int)a.E, tiles_per_head, a.out_f32 ? 1 : 0);
-  return hipGetLastError();
+  if constexpr (D == 64) {
+    // E split when the tiles fit on the CUs at one workgroup each (the unsplit kernel would
+    // leave a SIMD with one wave) and each part gets at least two chunks.
+    // FMLP_FWD_SPLIT (read once per process): 0 = never, 1 = whenever E allows, else this rule.
+    static const int force = env_int("FMLP_FWD_SPLIT", -1);
+    const bool fits = force == 1 || (force != 0 && grid <= a.num_cus);
+    if (fits && a.E > 64) return launch_fwd_e<BF16, D, ACT, 2>(a, tiles_per_head, grid, st);
+  }
+  return launch_fwd_e<BF16, D, ACT, 1>(a, tiles_per_head, grid, st);
 }
 
 template <bool BF16, int D>

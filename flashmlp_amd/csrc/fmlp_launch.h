@@ -25,6 +25,7 @@ struct FwdArgs {
   bool bf16;
   int act;
   bool out_f32;  // outputs as fp32 (FMLP_OUT_F32)
+  int num_cus;   // compute units of the current device
 };
 
 // Backward work decomposition (chosen on the host, see plan_bwd):
