@@ -129,8 +129,8 @@ __device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], void* __
 // Waves 0-3 run MFMA-then-VALU, waves 4-7 VALU(c-1)-then-MFMA, so the two waves sharing a
 // SIMD keep the matrix cores and the VALU busy at the same time (the per-chunk barrier
 // would otherwise align them). Nothing is double-buffered in registers, which keeps a wave
-// within 256 VGPRs. W1c / W2c chunks are staged through registers into a 4-slot LDS ring
-// (loaded one chunk ahead, stored at the start of the next chunk).
+// within 256 VGPRs. W1c / W2c chunks go straight from global memory into an 8-slot LDS ring
+// (buffer loads with the LDS destination, DX_PF = 4 chunks ahead of the chunk read).
 //
 // E-order inside a chunk: Z^T row m holds chunk column e = sig(m) (bits 2 and 3 of m
 // swapped). Then the 8 k-slots a lane holds of the dZ operand (C layout rows
