@@ -523,7 +523,11 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
   // 8 K-step-1 MFMAs follow.
   // per-head dZ resource (DZ): Bp / 256 tiles of [nE * 128 rows e][256 positions]
   const int Ep = nE * DW_ET;
-  const Rsrc rdz = make_rsrc(DZ ? dzt + (size_t)h * Ep * Bp : nullptr, DZ ? Ep * Bp * 2 : 0);
+  const u16* dzh = DZ ? dzt + (size_t)h * Ep * Bp : nullptr;
+  // lane part of the dZ store offsets inside a subtile's 2 KB block [32 columns][32 positions]
+  unsigned dzLane[2];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; ++s2) dzLane[s2] = ((unsigned)l32 * 32u + (unsigned)(16 * s2 + 8 * g)) * 2u;
   auto ag2_phase = [&](int slot, int rbase) {
     const int base2 = RING_OFF + slot * PAIR;
     auto fetch = [&](int q) -> u32x4 {  // (s, nt, which): which 0 -> dW2 (B = dO^T), 1 -> dW1^T (B = X^T)
@@ -570,15 +574,15 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
     if constexpr (DZ) {
       // dzT[s] holds rows 16 s + 4 g + 0..3 and 16 s + 8 + 4 g + 0..3 of column e0 + l32: positions
       // 16 s + 8 g .. + 7 under sig, one 16-byte store each; subtiles past the program's rows
-      // (the odd last one of a B range) store nothing (out-of-range offset)
+      // (the odd last one of a B range) store nothing (an empty resource). The block base and
+      // that test are wave-uniform, so they live in the resource (scalar registers) and each
+      // lane's offset is a constant.
       const bool live = rbase < b_hi;
       const unsigned blk = ((unsigned)(rbase >> 8) * (unsigned)(Ep >> 5) + (unsigned)(e0 >> 5)) * 8u +
                            (unsigned)((rbase & 255) >> 5);
+      const Rsrc rb = make_rsrc(dzh + (size_t)blk * 1024u, live ? 2048 : 0);
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const unsigned off = ((blk * 32u + (unsigned)l32) * 32u + (unsigned)(16 * s2 + 8 * g)) * 2u;
-        __builtin_amdgcn_raw_buffer_store_b128(dzT[s2], rdz, live ? off : BUF_OOB, 0, 0);
-      }
+      for (int s2 = 0; s2 < 2; ++s2) __builtin_amdgcn_raw_buffer_store_b128(dzT[s2], rb, (int)dzLane[s2], 0, 0);
     }
   };
   // end of a pair: this wave's loads of the next pair have landed; the barrier publishes

@@ -196,8 +196,13 @@ __device__ __forceinline__ Rsrc make_rsrc(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, __builtin_amdgcn_readfirstlane(bytes),
                                            0x00020000);
 }
-// min(max(v, 0), hi) with scalar-unit friendly selects (v, hi wave-uniform)
-__device__ __forceinline__ int clamp0(int v, int hi) { return v < 0 ? 0 : (v > hi ? hi : v); }
+// min(max(v, 0), hi) for wave-uniform v and hi. The readfirstlane between the two selects
+// keeps the compiler from fusing them into a vector v_med3 (plus a readfirstlane back): the
+// clamp stays two scalar instructions, off the VALU that the kernel loops are bound by.
+__device__ __forceinline__ int clamp0(int v, int hi) {
+  const int t = __builtin_amdgcn_readfirstlane(v < 0 ? 0 : v);
+  return __builtin_amdgcn_readfirstlane(t > hi ? hi : t);
+}
 __device__ __forceinline__ u32x4 buf_load16(Rsrc r, unsigned byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
 }
