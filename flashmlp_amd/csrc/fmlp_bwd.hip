@@ -91,35 +91,6 @@ __device__ __forceinline__ void dw_store(const f32x16 (&a1)[D / 32], const f32x1
   }
 }
 
-// Store of a wave's 32-row dX tile (C layout: lane = column d = 32 nt + l32, rows
-// b0 + 8 (i / 4) + 4 g + (i % 4)); rows at or past B are not written.
-template <bool BF16, int D>
-__device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], void* __restrict__ out, size_t head_off, int B,
-                                           int b0, int g, int l32, int outf32) {
-  constexpr int NTN = D / 32;
-  if (outf32) {
-    float* o = (float*)out + head_off;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int b = b0 + 8 * (i >> 2) + 4 * g + (i & 3);
-      if (b < B) {
-#pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) o[(size_t)b * D + nt * 32 + l32] = acc[nt][i];
-      }
-    }
-  } else {
-    u16* o = (u16*)out + head_off;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int b = b0 + 8 * (i >> 2) + 4 * g + (i & 3);
-      if (b < B) {
-#pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) o[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(acc[nt][i]);
-      }
-    }
-  }
-}
-
 // ------------------------------------------------------------------------------------
 // dX programs, two-waves-per-SIMD form (dx2_kernel): 8 waves x 32 rows = 256 rows of one
 // head. Per 32-column E-chunk c each wave runs two phases:

@@ -203,6 +203,39 @@ __device__ __forceinline__ int clamp0(int v, int hi) {
   const int t = __builtin_amdgcn_readfirstlane(v < 0 ? 0 : v);
   return __builtin_amdgcn_readfirstlane(t > hi ? hi : t);
 }
+// Store of a wave's 32-row output tile in the MFMA C layout (lane = column 32 nt + l32 of a
+// [rows][D] row-major tensor, rows b0 + 8 (i / 4) + 4 g + (i % 4) in acc[nt][i]), as the io
+// dtype or, with outf32, as the fp32 sums. b0 is wave-uniform: the wave's rows get a buffer
+// resource of their own, so rows at or past B fall outside it (no branches), and each
+// store's offset is one of four lane registers (one per 8-row group) plus a constant in the
+// instruction's offset field (at most (3 D + 96) 4 bytes < 4096).
+template <bool BF16, int D>
+__device__ __forceinline__ void store_rows(const f32x16 (&acc)[D / 32], void* __restrict__ out, size_t head_off, int B,
+                                           int b0, int g, int l32, int outf32) {
+  constexpr int NTN = D / 32;
+  static_assert((3 * D + 96) * 4 < 4096, "store offsets within the immediate field");
+  const int rows = clamp0(B - b0, 32);
+  const int es = outf32 ? 4 : 2;
+  const Rsrc r = make_rsrc((const char*)out + (head_off + (size_t)b0 * D) * es, rows * D * es);
+  unsigned vo[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) vo[q] = (unsigned)((8 * q + 4 * g) * D + l32) * (unsigned)es;
+  if (outf32) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(acc[nt][i]), r,
+                                              (int)(vo[i >> 2] + (unsigned)(((i & 3) * D + nt * 32) * 4)), 0, 0);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt)
+        __builtin_amdgcn_raw_buffer_store_b16(from_f32<BF16>(acc[nt][i]), r,
+                                              (int)(vo[i >> 2] + (unsigned)(((i & 3) * D + nt * 32) * 2)), 0, 0);
+  }
+}
 __device__ __forceinline__ u32x4 buf_load16(Rsrc r, unsigned byte_off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, 0, 0);
 }

@@ -273,27 +273,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   }
   // ---- epilogue: O tile (C layout: lane = column d, rows 8(i/4) + 4g + i%4); fp32 sums
   // when the caller asked for them (FMLP_OUT_F32), else rounded to the io dtype ----
-  if (outf32) {
-    float* Oh = (float*)O + (size_t)h * B * D;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int b = b_wave + 8 * (i >> 2) + 4 * g + (i & 3);
-      if (b < B) {
-#pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) Oh[(size_t)b * D + nt * 32 + l32] = o[nt][i];
-      }
-    }
-  } else {
-    u16* Oh = (u16*)O + (size_t)h * B * D;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int b = b_wave + 8 * (i >> 2) + 4 * g + (i & 3);
-      if (b < B) {
-#pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) Oh[(size_t)b * D + nt * 32 + l32] = from_f32<BF16>(o[nt][i]);
-      }
-    }
-  }
+  store_rows<BF16, D>(o, O, (size_t)h * B * D, B, b_wave, g, l32, outf32);
 }
 
 // ------------------------------------------------------------------------------------
