@@ -357,8 +357,9 @@ def main():
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(json.dumps({"error": "this build measures one GPU; the fused MLP shards by head with no "
-                                   "communication (see DESIGN.md), multi-GPU runs are not part of it",
+        print(json.dumps({"error": "this build measures one GPU: the fused MLP shards by head with no "
+                                   "communication (each GPU runs its heads' share as one GPU does here), "
+                                   "so multi-GPU runs are not part of it",
                           "n_gpus": args.gpus}), flush=True)
         sys.exit(2)
 
