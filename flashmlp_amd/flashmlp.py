@@ -79,6 +79,11 @@ def _dense(t: torch.Tensor) -> torch.Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+def _alloc_ws(nbytes: int, device: torch.device):
+    # the backward's workspace (None when the plan needs none)
+    return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
+
+
 @functools.lru_cache(maxsize=1024)
 def _tuned(D: int, E: int, dtype: int) -> bool:
     return bool(_lib.lib().fmlp_shape_tuned(D, E, dtype))
@@ -128,7 +133,8 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     Returns (dx, dw1, dw2) shaped like (x, w1, w2). For large shapes the library stores dZ in
     a temporary workspace (H x ceil(E/128)*128 x ceil(B/256)*256 io elements) and computes dx
     from it; recompute=True keeps the reference's recompute-only form, whose extra memory is
-    at most the fp32 dW partials. accurate_dw=True takes h and dZ into the dW products as
+    at most the fp32 dW partials, and it is also taken when the stored-dZ workspace cannot be
+    allocated. accurate_dw=True takes h and dZ into the dW products as
     hi + lo io-dtype terms. Both keywords have no counterpart in the reference.
     """
     assert x.shape[0] == w1.shape[0], "Number of heads must match"
@@ -151,9 +157,18 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
         stream = torch.cuda.current_stream(x.device).cuda_stream
         if _tuned(D, E, dtype):
             x, w1, w2, do = _dense(x), _dense(w1), _dense(w2), _dense(do)
-            ws_bytes = _ws_bytes(x.device.index if x.device.index is not None else torch.cuda.current_device(),
-                                 H, B, D, E, flags)
-            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+            dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
+            ws_bytes = _ws_bytes(dev, H, B, D, E, flags)
+            try:
+                ws = _alloc_ws(ws_bytes, x.device)
+            except torch.OutOfMemoryError:
+                if flags & _lib.FMLP_BWD_RECOMPUTE:
+                    raise
+                # the stored-dZ form's workspace does not fit: the recompute form needs at most
+                # the fp32 dW partials (the reference's backward allocates no workspace at all)
+                flags |= _lib.FMLP_BWD_RECOMPUTE
+                ws_bytes = _ws_bytes(dev, H, B, D, E, flags)
+                ws = _alloc_ws(ws_bytes, x.device)
             st = L.fmlp_bwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(),
                             dw1.data_ptr(), dw2.data_ptr(), H, B, D, E, flags, _act_code(activation),
                             ws.data_ptr() if ws is not None else None, ws_bytes, stream)

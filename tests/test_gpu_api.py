@@ -145,3 +145,34 @@ def test_leaky_relu_zero_point_follows_autograd():
     _, rdx, rdw1, rdw2 = reference.autograd_grads(x, w1, w2, do, "leaky_relu")
     torch.testing.assert_close(dx.float().cpu(), rdx, **TOL)
     assert rdx[:, ::7].abs().max() > 0
+
+
+def test_bwd_falls_back_to_recompute_when_workspace_does_not_fit(monkeypatch):
+    """flashmlp_bwd takes the recompute form when the stored-dZ workspace cannot be allocated
+    (the reference's backward allocates no workspace): same results as recompute=True."""
+    import importlib
+
+    from flashmlp_amd import _lib
+
+    fmm = importlib.import_module("flashmlp_amd.flashmlp")
+    H, B, D, E, dt, act = 8, 4097, 64, 2048, torch.float16, "sigmoid"
+    code, act_code = _lib.FMLP_DTYPE_F16, _lib.ACT_CODES[act]
+    assert _lib.lib().fmlp_bwd_stores_dz(H, B, D, E, code, act_code) == 1, "this shape should take the stored-dZ form"
+    assert _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, code | _lib.FMLP_BWD_RECOMPUTE) < (64 << 20)
+    _say(f"[api] workspace fallback H={H} B={B} D={D} E={E} {dt} act='{act}'")
+    x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=61))
+    ref = fm.flashmlp_bwd(x, w1, w2, do, act, recompute=True)
+    real, sizes = fmm._alloc_ws, []
+
+    def tight(nbytes, device):  # a device with less than 64 MiB free
+        sizes.append(nbytes)
+        if nbytes > (64 << 20):
+            raise torch.OutOfMemoryError("simulated: workspace does not fit")
+        return real(nbytes, device)
+
+    monkeypatch.setattr(fmm, "_alloc_ws", tight)
+    got = fm.flashmlp_bwd(x, w1, w2, do, act)
+    torch.cuda.synchronize()
+    assert len(sizes) == 2 and sizes[0] > (64 << 20) >= sizes[1]
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
