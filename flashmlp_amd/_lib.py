@@ -23,6 +23,9 @@ FMLP_DW_HILO = 0x200
 FMLP_BWD_RECOMPUTE = 0x400
 # OR-ed into the backward's dtype code: the stored-dZ form whenever the workspace allows (tests)
 FMLP_BWD_STORE_DZ = 0x800
+# OR-ed into the backward's dtype code: no dx wanted (dx may be NULL) / no dw1, dw2 wanted
+FMLP_BWD_NO_DX = 0x1000
+FMLP_BWD_NO_DW = 0x2000
 ACT_CODES = {"": 0, "silu": 1, "leaky_relu": 2, "sigmoid": 3}
 
 # (name, restype, argtypes) for every symbol include/flashmlp.h declares

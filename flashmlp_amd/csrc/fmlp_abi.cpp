@@ -76,11 +76,15 @@ int num_cus_current(int* out) {
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // io dtype of a dtype argument (its flag bits removed)
-int io_of(int dtype) { return dtype & ~(FMLP_OUT_F32 | FMLP_DW_HILO | FMLP_BWD_RECOMPUTE | FMLP_BWD_STORE_DZ); }
+int io_of(int dtype) {
+  return dtype & ~(FMLP_OUT_F32 | FMLP_DW_HILO | FMLP_BWD_RECOMPUTE | FMLP_BWD_STORE_DZ | FMLP_BWD_NO_DX | FMLP_BWD_NO_DW);
+}
 
 // backward form selection from the dtype flags (plan_bwd's dz_mode)
+// (a partial backward, FMLP_BWD_NO_DX / FMLP_BWD_NO_DW, runs the recompute form's programs)
 int dz_mode_of(int dtype) {
-  return (dtype & FMLP_BWD_RECOMPUTE) ? fmlp::DZ_NEVER : (dtype & FMLP_BWD_STORE_DZ) ? fmlp::DZ_FORCE : fmlp::DZ_AUTO;
+  if (dtype & (FMLP_BWD_RECOMPUTE | FMLP_BWD_NO_DX | FMLP_BWD_NO_DW)) return fmlp::DZ_NEVER;
+  return (dtype & FMLP_BWD_STORE_DZ) ? fmlp::DZ_FORCE : fmlp::DZ_AUTO;
 }
 size_t elem_bytes(int io) { return io == FMLP_DTYPE_F32 ? 4 : 2; }
 
@@ -213,8 +217,9 @@ namespace {
 int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D, int64_t E,
              const int64_t* sx, const int64_t* sw1, const int64_t* sw2, int dtype, int act, void* stream) {
   if (dtype & FMLP_DW_HILO) return fail(FMLP_ERR_INVALID_ARG, "FMLP_DW_HILO applies to the backward only");
-  if (dtype & (FMLP_BWD_RECOMPUTE | FMLP_BWD_STORE_DZ))
-    return fail(FMLP_ERR_INVALID_ARG, "FMLP_BWD_RECOMPUTE / FMLP_BWD_STORE_DZ apply to the backward only");
+  if (dtype & (FMLP_BWD_RECOMPUTE | FMLP_BWD_STORE_DZ | FMLP_BWD_NO_DX | FMLP_BWD_NO_DW))
+    return fail(FMLP_ERR_INVALID_ARG,
+                "FMLP_BWD_RECOMPUTE / FMLP_BWD_STORE_DZ / FMLP_BWD_NO_DX / FMLP_BWD_NO_DW apply to the backward only");
   int st = check_shape(H, B, D, E, dtype);
   if (st) return st;
   if ((st = check_act(act))) return st;
@@ -305,13 +310,14 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
     return st;
   const bool rows = H > 0 && B > 0;
   const bool wts = H > 0;
+  const bool want_dx = (dtype & FMLP_BWD_NO_DX) == 0, want_dw = (dtype & FMLP_BWD_NO_DW) == 0;
   const int io = io_of(dtype);
   const size_t es = elem_bytes(io), os = (dtype & FMLP_OUT_F32) ? 4 : es;
   if ((st = check_ptr(x, "x", rows, es)) || (st = check_ptr(w1, "w1", wts, es)) || (st = check_ptr(w2, "w2", wts, es)) ||
-      (st = check_ptr(dout, "dout", rows, es)) || (st = check_ptr(dx, "dx", rows, os)) ||
-      (st = check_ptr(dw1, "dw1", wts, os)) || (st = check_ptr(dw2, "dw2", wts, os)))
+      (st = check_ptr(dout, "dout", rows, es)) || (st = check_ptr(dx, "dx", rows && want_dx, os)) ||
+      (st = check_ptr(dw1, "dw1", wts && want_dw, os)) || (st = check_ptr(dw2, "dw2", wts && want_dw, os)))
     return st;
-  if (H == 0) return ok();
+  if (H == 0 || (!want_dx && !want_dw)) return ok();
   const bool dense = sx == nullptr || (is_dense3(sx, B, D) && is_dense3(sw1, D, E) && is_dense3(sw2, E, D) &&
                                        is_dense3(sdo, B, D));
   const bool aligned = aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(dout) && aligned16(dx) &&
@@ -339,10 +345,12 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
       }
     }
     fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io == FMLP_DTYPE_BF16, act, ws,
-                    (dtype & FMLP_OUT_F32) != 0, (dtype & FMLP_DW_HILO) != 0};
+                    (dtype & FMLP_OUT_F32) != 0, (dtype & FMLP_DW_HILO) != 0, want_dx, want_dw};
     e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
   } else {
     fmlp::GenArgs g = gen_args(x, w1, w2, dout, nullptr, dx, dw1, dw2, H, B, D, E, dtype, act);
+    g.want_dx = want_dx ? 1 : 0;
+    g.want_dw = want_dw ? 1 : 0;
     if (sx) {
       for (int i = 0; i < 3; ++i) {
         g.sx[i] = sx[i];

@@ -1116,7 +1116,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
                        a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
     return hipGetLastError();
   };
-  if (p.dz) {  // stored-dZ form: dW programs storing dZ, their reduction, then the dX GEMM
+  if (p.dz && a.want_dx && a.want_dw) {  // stored-dZ form: dW programs storing dZ, their reduction, then the dX GEMM
     u16* dzt = (u16*)((char*)a.ws + p.dz_off);
     const int Ep = p.nE * DW_ET;
     auto launch_w = [&](auto k) {
@@ -1142,7 +1142,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   // FMLP_BWD_UNIFIED (read once per process): 1 (default) = one launch holding both roles,
   // 0 = dW programs (and their reduction), then dX programs, as separate launches
   static const int unified = env_int("FMLP_BWD_UNIFIED", 1);
-  if (unified && p.n_dw > 0 && p.n_dx > 0) {
+  // a partial backward (FMLP_BWD_NO_DX / FMLP_BWD_NO_DW) launches only the programs it needs
+  if (unified && a.want_dx && a.want_dw && p.n_dw > 0 && p.n_dx > 0) {
     auto launch_u = [&](auto k) {
       static std::atomic<unsigned long long> lds_set{0};
       hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
@@ -1157,7 +1158,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     if (e != hipSuccess) return e;
     return reduce();
   }
-  if (p.n_dw > 0) {
+  if (p.n_dw > 0 && a.want_dw) {
     auto launch_w = [&](auto k) {
       static std::atomic<unsigned long long> lds_set{0};
       hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
@@ -1171,7 +1172,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     if (e != hipSuccess) return e;
     if ((e = reduce()) != hipSuccess) return e;
   }
-  if (p.n_dx > 0) {
+  if (p.n_dx > 0 && a.want_dx) {
     const size_t lds_x = (size_t)DX_NSLOT * 128u * D;  // the chunk ring
     auto k = dx2_kernel<BF16, D, ACT>;
     static std::atomic<unsigned long long> lds_set{0};

@@ -437,12 +437,12 @@ hipError_t gen_launch_bwd_t(const GenArgs& a, hipStream_t st) {
   const long long tph = (a.B + GEN_ROWS - 1) / GEN_ROWS;
   const long long ctph = (a.E + GEN_COLS - 1) / GEN_COLS;
   if (tph * a.H > 0x7fffffffLL || ctph * a.H > 0x7fffffffLL) return hipErrorInvalidValue;
-  if (a.H > 0 && ctph > 0) {
+  if (a.H > 0 && ctph > 0 && a.want_dw) {
     hipLaunchKernelGGL((gen_dw_kernel<IO, D>), dim3((unsigned)(ctph * a.H)), dim3(GEN_NT), 0, st, a, (int)ctph);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (a.H > 0 && tph > 0) {
+  if (a.H > 0 && tph > 0 && a.want_dx) {
     hipLaunchKernelGGL((gen_dx_kernel<IO, D>), dim3((unsigned)(tph * a.H)), dim3(GEN_NT), 0, st, a, (int)tph);
     return hipGetLastError();
   }

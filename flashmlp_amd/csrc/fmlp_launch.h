@@ -63,6 +63,8 @@ struct BwdArgs {
   void* ws;
   bool out_f32;  // outputs as fp32 (FMLP_OUT_F32)
   bool dw_hilo;  // dW products with hi/lo terms of h and dZ (FMLP_DW_HILO)
+  bool want_dx = true;  // false: FMLP_BWD_NO_DX (only the dW programs run)
+  bool want_dw = true;  // false: FMLP_BWD_NO_DW (only the dX programs run)
 };
 
 // io element types of the generic kernels
@@ -85,6 +87,7 @@ struct GenArgs {
   int act;
   int out_f32;  // outputs as fp32 (FMLP_OUT_F32)
   int hilo;     // dW products with hi/lo terms of h and dZ (FMLP_DW_HILO; 16-bit io)
+  int want_dx = 1, want_dw = 1;  // FMLP_BWD_NO_DX / FMLP_BWD_NO_DW clear them
 };
 hipError_t launch_gen_fwd(const GenArgs& a, hipStream_t st);
 hipError_t launch_gen_bwd(const GenArgs& a, hipStream_t st);

@@ -79,6 +79,11 @@ def _dense(t: torch.Tensor) -> torch.Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
+def _ptr(t):
+    # device address of an output, or NULL for one that is not computed
+    return t.data_ptr() if t is not None else None
+
+
 def _alloc_ws(nbytes: int, device: torch.device):
     # the backward's workspace (None when the plan needs none)
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
@@ -125,8 +130,8 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
 
 
 def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.Tensor,
-                 activation: str = "", *, accurate_dw: bool = False,
-                 recompute: bool = False) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+                 activation: str = "", *, accurate_dw: bool = False, recompute: bool = False,
+                 _needs: Tuple[bool, bool] = (True, True)) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """FlashMLP backward pass (reference: flashmlp.py:480-538).
 
     Recomputes Z = x @ w1 and h = act(Z) instead of reading stored activations.
@@ -135,7 +140,9 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     from it; recompute=True keeps the reference's recompute-only form, whose extra memory is
     at most the fp32 dW partials, and it is also taken when the stored-dZ workspace cannot be
     allocated. accurate_dw=True takes h and dZ into the dW products as
-    hi + lo io-dtype terms. Both keywords have no counterpart in the reference.
+    hi + lo io-dtype terms. Both keywords have no counterpart in the reference. `_needs`
+    (need dx, need dw1 and dw2; FlashMLPFunction passes autograd's needs_input_grad) skips the
+    programs of a gradient nobody asked for and returns None in its place.
     """
     assert x.shape[0] == w1.shape[0], "Number of heads must match"
     assert x.shape[0] == w2.shape[0], "Number of heads must match"
@@ -148,10 +155,14 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     E = w1.shape[2]
 
     dtype = _check_tensors(x, w1, w2, do)
+    need_dx, need_dw = bool(_needs[0]), bool(_needs[1])
     flags = dtype | (_lib.FMLP_DW_HILO if accurate_dw else 0) | (_lib.FMLP_BWD_RECOMPUTE if recompute else 0)
-    dx = torch.empty((H, B, D), dtype=x.dtype, device=x.device)
-    dw1 = torch.empty((H, D, E), dtype=x.dtype, device=x.device)
-    dw2 = torch.empty((H, E, D), dtype=x.dtype, device=x.device)
+    flags |= (0 if need_dx else _lib.FMLP_BWD_NO_DX) | (0 if need_dw else _lib.FMLP_BWD_NO_DW)
+    dx = torch.empty((H, B, D), dtype=x.dtype, device=x.device) if need_dx else None
+    dw1 = torch.empty((H, D, E), dtype=x.dtype, device=x.device) if need_dw else None
+    dw2 = torch.empty((H, E, D), dtype=x.dtype, device=x.device) if need_dw else None
+    if not (need_dx or need_dw):
+        return dx, dw1, dw2
     L = _lib.lib()
     with torch.cuda.device(x.device):
         stream = torch.cuda.current_stream(x.device).cuda_stream
@@ -169,12 +180,12 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
                 flags |= _lib.FMLP_BWD_RECOMPUTE
                 ws_bytes = _ws_bytes(dev, H, B, D, E, flags)
                 ws = _alloc_ws(ws_bytes, x.device)
-            st = L.fmlp_bwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(),
-                            dw1.data_ptr(), dw2.data_ptr(), H, B, D, E, flags, _act_code(activation),
+            st = L.fmlp_bwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), _ptr(dx),
+                            _ptr(dw1), _ptr(dw2), H, B, D, E, flags, _act_code(activation),
                             ws.data_ptr() if ws is not None else None, ws_bytes, stream)
         else:
-            st = L.fmlp_bwd_strided(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), dx.data_ptr(),
-                                    dw1.data_ptr(), dw2.data_ptr(), H, B, D, E, _lib.strides(x), _lib.strides(w1),
+            st = L.fmlp_bwd_strided(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), _ptr(dx),
+                                    _ptr(dw1), _ptr(dw2), H, B, D, E, _lib.strides(x), _lib.strides(w1),
                                     _lib.strides(w2), _lib.strides(do), flags, _act_code(activation), None, 0,
                                     stream)
     _lib.check(st, "backward")
@@ -195,8 +206,12 @@ class FlashMLPFunction(torch.autograd.Function):
     @staticmethod
     def backward(ctx, do):
         x, w1, w2 = ctx.saved_tensors
-        dx, dw1, dw2 = flashmlp_bwd(x, w1, w2, do, ctx.activation, accurate_dw=ctx.accurate_dw)
-        return dx, dw1, dw2, None, None
+        need_x, need_w1, need_w2 = ctx.needs_input_grad[:3]
+        # only the programs of the gradients autograd asks for run (an input or weights that
+        # need no gradient skip the dX or the dW programs)
+        dx, dw1, dw2 = flashmlp_bwd(x, w1, w2, do, ctx.activation, accurate_dw=ctx.accurate_dw,
+                                    _needs=(need_x, need_w1 or need_w2))
+        return dx, (dw1 if need_w1 else None), (dw2 if need_w2 else None), None, None
 
 
 class FlashMLP(torch.nn.Module):

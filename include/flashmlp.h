@@ -73,6 +73,16 @@ typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1, FMLP_DTYPE_F32 = 2 } fml
  * the same shapes). */
 #define FMLP_BWD_STORE_DZ 0x800
 
+/* OR-ed into the dtype argument of fmlp_bwd / fmlp_bwd_strided / fmlp_bwd_noalloc: the caller
+ * needs no dx (FMLP_BWD_NO_DX: dx may be NULL and is not written; only the dW programs run, in
+ * the recompute form's plan) or no dw1, dw2 (FMLP_BWD_NO_DW: both may be NULL and are not
+ * written; only the dX programs run). The results that are computed are bit-identical to the
+ * recompute form's (FMLP_BWD_RECOMPUTE). No counterpart in the reference, whose backward
+ * always computes all three: for autograd callers whose input, or whose weights, need no
+ * gradient. Both flags together: nothing to compute. */
+#define FMLP_BWD_NO_DX 0x1000
+#define FMLP_BWD_NO_DW 0x2000
+
 /* Activation codes; names as in the reference ("", "silu", "leaky_relu", "sigmoid"). */
 typedef enum { FMLP_ACT_NONE = 0, FMLP_ACT_SILU = 1, FMLP_ACT_LEAKY_RELU = 2, FMLP_ACT_SIGMOID = 3 } fmlp_act;
 

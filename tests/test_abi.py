@@ -84,7 +84,8 @@ def test_shape_support(L):
     assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_BWD_RECOMPUTE) == 1
     assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_BWD_STORE_DZ) == 1
     assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_BWD_STORE_DZ | _lib.FMLP_BWD_RECOMPUTE) == 0
-    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | 0x1000) == 0
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | _lib.FMLP_BWD_NO_DX | _lib.FMLP_BWD_NO_DW) == 1
+    assert L.fmlp_shape_supported(2, 8, 64, 64, 1 | 0x4000) == 0  # an unknown flag bit
     assert L.fmlp_shape_supported(-1, 8, 64, 64, 1) == 0
 
 
@@ -149,6 +150,13 @@ def test_backward_argument_validation(L):
     assert bwd(H=2, B=8192, D=128, E=128) in (WORKSPACE, HIPERR)
     assert bwd(act=-1) == INVALID
     assert bwd(H=0, x=None, do=None, dx=None) == OK
+    # FMLP_BWD_NO_DX / FMLP_BWD_NO_DW: the unwanted outputs may be NULL (the argument checks pass;
+    # without a GPU the CU-count query fails next), the wanted ones may not; both: nothing to do
+    assert bwd(dx=None, dtype=1 | _lib.FMLP_BWD_NO_DX) in (OK, HIPERR)
+    assert bwd(dw1=None, dw2=None, dtype=1 | _lib.FMLP_BWD_NO_DW) in (OK, HIPERR)
+    assert bwd(dx=None, dtype=1 | _lib.FMLP_BWD_NO_DW) == INVALID
+    assert bwd(dx=None, dw1=None, dw2=None, dtype=1 | _lib.FMLP_BWD_NO_DX | _lib.FMLP_BWD_NO_DW) == OK
+    assert _fwd(L, dtype=1 | _lib.FMLP_BWD_NO_DX) == INVALID  # a backward-only flag
 
 
 def test_workspace_query_is_zero_for_invalid_shapes(L):

@@ -176,3 +176,32 @@ def test_bwd_falls_back_to_recompute_when_workspace_does_not_fit(monkeypatch):
     assert len(sizes) == 2 and sizes[0] > (64 << 20) >= sizes[1]
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("H,B,D,E,dt,act", [
+    (2, 4096, 128, 512, torch.bfloat16, "silu"),       # tuned kernels, B split of the dW programs
+    (8, 4097, 64, 2048, torch.float16, "sigmoid"),     # tuned kernels, B and dX-tile tails
+    (3, 300, 32, 45, torch.float16, "leaky_relu"),     # generic kernels
+], ids=["bf16-D128", "fp16-D64-tail", "fp16-D32-generic"])
+def test_function_computes_only_the_gradients_autograd_needs(H, B, D, E, dt, act):
+    """FlashMLPFunction passes autograd's needs_input_grad down (FMLP_BWD_NO_DX / FMLP_BWD_NO_DW):
+    an input or weights that need no gradient skip the dX or the dW programs, and what is
+    computed is bit-identical to the recompute form's full backward."""
+    _say(f"[api] partial backward H={H} B={B} D={D} E={E} {dt} act='{act}'")
+    x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=62))
+    dx, dw1, dw2 = fm.flashmlp_bwd(x, w1, w2, do, act, recompute=True)
+    # the input needs no gradient: dW programs only
+    w1g, w2g = w1.clone().requires_grad_(True), w2.clone().requires_grad_(True)
+    fm.FlashMLPFunction.apply(x, w1g, w2g, act).backward(do)
+    assert torch.equal(w1g.grad, dw1) and torch.equal(w2g.grad, dw2)
+    # frozen weights: dX programs only
+    xg = x.clone().requires_grad_(True)
+    fm.FlashMLPFunction.apply(xg, w1, w2, act).backward(do)
+    assert torch.equal(xg.grad, dx)
+    # one weight needs a gradient: the dW programs run, only that gradient is returned
+    w2h = w2.clone().requires_grad_(True)
+    fm.FlashMLPFunction.apply(x, w1, w2h, act).backward(do)
+    assert torch.equal(w2h.grad, dw2)
+    # the low-level function with nothing needed returns no tensors and launches nothing
+    assert fm.flashmlp_bwd(x, w1, w2, do, act, _needs=(False, False)) == (None, None, None)
+    torch.cuda.synchronize()
