@@ -75,7 +75,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.restype = res
                 fn.argtypes = args
-            if handle.fmlp_abi_version() != 1:
+            if handle.fmlp_abi_version() != 2:
                 raise FlashMLPLibraryError("libflashmlp.so ABI version mismatch; rebuild it")
             _lib = handle
     return _lib

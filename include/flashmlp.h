@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define FMLP_ABI_VERSION 1
+#define FMLP_ABI_VERSION 2  /* 2: FMLP_BWD_NO_DX / FMLP_BWD_NO_DW */
 
 typedef enum {
   FMLP_OK = 0,
