@@ -11,10 +11,24 @@ FLOP accounting: u = H*B*D*E; forward 4u, backward 8u, step 12u.
 launch, the backward entry point fmlp_bwd (8u algorithmic FLOPs per call; the forward for
 cfg5s), with its duration from HIP events recorded on the stream the kernels run on.
 Algorithmic HBM bytes at s bytes per element: forward (2 HBD + 2 HDE) s, backward
-(3 HBD + 4 HDE) s. `autograd_ms_per_step` times the module-level step the reference's
-example.py:120-128 times (FlashMLPFunction forward, then .backward). `cpu_baseline` times
-the CPU oracle (torch fp32 autograd of the restated reference path) on a bounded sample of
-the same workload, plus the reference's CPU configuration (cfg1) in full.
+(3 HBD + 4 HDE) s.
+
+The default (cfg4) line also carries, measured in the same process after the headline:
+  * `cfg4_forms`: the same step with the reference's recompute-only backward (recompute=True,
+    the form the north star names), with the dW accuracy mode (accurate_dw=True: dW within the
+    elementwise tolerance of fp32), and with both;
+  * `configs`: every other BASELINE.json configuration (cfg2, cfg3, cfg5 sigmoid and linear,
+    the forward-only cfg5s sweep) on the tuned kernels, and two shapes of the generic kernels
+    (the reference's CPU configuration cfg1 in fp32, and D = 256);
+  * `vs_pytorch_unfused`: the unfused PyTorch path (bmm -> activation -> bmm, the (H, B, E)
+    intermediates kept, manual backward) on the same GPU against FlashMLP, at cfg4 and at the
+    four shapes of the reference's performance.md (example.py:98-135 compares the two);
+  * `memory`: peak allocated MB of one fwd+bwd for both backward forms and the unfused path
+    (example.py:142-200), plus the device memory the library's code objects hold;
+  * `autograd_ms_per_step` (FlashMLPFunction forward + backward, as example.py:120-128 times
+    the module), host microseconds per call;
+  * `cpu_baseline`: the CPU oracle (torch fp32 autograd of the restated reference path) on a
+    bounded sample of the workload, plus the reference's CPU configuration (cfg1) in full.
 
 Other workloads: cfg2, cfg3, cfg5, cfg5_linear (fwd+bwd), cfg5s
 (forward-only, reports HBM GB/s), example (the four shapes of the reference's
@@ -25,6 +39,7 @@ waves per SIMD, random and all-zero operands; libfmlp_ceiling.so).
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -36,7 +51,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "fwd+bwd TFLOP/s and % of MFMA peak (bf16/fp16), H=32 B=16384 D=128 E=1024"
-PEAK_TFLOPS = {"bf16": 2516.6, "f16": 2516.6}  # MI355X dense MFMA, 256 CU x 2.4 GHz x 4096 FLOP/clk
+# MI355X dense MFMA peaks (256 CU x 2.4 GHz): bf16 / fp16 4096 FLOP/clk/CU, fp32 256
+PEAK_TFLOPS = {"bf16": 2516.6, "f16": 2516.6, "f32": 157.3}
 HBM_GBS = 8000.0
 
 WORKLOADS = {
@@ -47,7 +63,12 @@ WORKLOADS = {
     "cfg5": (8, 4097, 64, 2048, "f16", "sigmoid", 2.0, False),
     "cfg5_linear": (8, 4097, 64, 2048, "f16", "", 2.0, False),
     "cfg5s": (8, 65536, 64, 2048, "f16", "sigmoid", 2.0, True),
+    # generic kernels: the reference's CPU configuration in fp32, D = 256
+    "cfg1_fp32": (12, 1024, 64, 768, "f32", "silu", 1.0, False),
+    "d256": (8, 4096, 256, 1024, "bf16", "silu", 1.0, False),
 }
+# the `configs` pass of the default line, in this order
+CONFIG_PASS = ["cfg2", "cfg3", "cfg5", "cfg5_linear", "cfg5s", "cfg1_fp32", "d256"]
 # performance.md:9-12 (example.py:86-91): bf16, SiLU, timed through the FlashMLP module
 EXAMPLE_SHAPES = [(8, 512, 64, 512), (12, 1024, 64, 768), (16, 2048, 64, 1024), (32, 4096, 64, 512)]
 EXAMPLE_PUBLISHED_MS = {  # (fwd, fwd+bwd) of the reference on its (unstated) hardware
@@ -59,7 +80,11 @@ EXAMPLE_PUBLISHED_MS = {  # (fwd, fwd+bwd) of the reference on its (unstated) ha
 def _torch_dtype(name):
     import torch
 
-    return {"bf16": torch.bfloat16, "f16": torch.float16}[name]
+    return {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[name]
+
+
+def _es(name):
+    return 4 if name == "f32" else 2
 
 
 def make_gpu_inputs(H, B, D, E, dtype, x_std, seed=0):
@@ -144,12 +169,62 @@ def cpu_baseline(H, B, D, E, activation, x_std, budget_s=10.0):
     }
 
 
+# ---------------------------------------------------------------------------------------
+# The unfused PyTorch path (the reference's PyTorchMLP / flashmlp_torch_bwd computation,
+# flashmlp.py:619-723): Z and h kept from the forward, the backward's products as bmm calls on
+# contiguous operands (transposed views are copied first; with the transposes placed so that
+# only weight-sized and X/dO-sized copies are made, never a copy of the (H, B, E) plane).
+# ---------------------------------------------------------------------------------------
+def _torch_act(t, activation):
+    import torch
+
+    return {"silu": torch.nn.functional.silu, "sigmoid": torch.sigmoid,
+            "leaky_relu": lambda v: torch.nn.functional.leaky_relu(v, 0.01)}.get(activation, lambda v: v)(t)
+
+
+def unfused_fwd(x, w1, w2, activation):
+    import torch
+
+    z = torch.bmm(x, w1)
+    h = _torch_act(z, activation)
+    return torch.bmm(h, w2), z, h
+
+
+def unfused_bwd(x, w1, w2, do, z, h, activation):
+    import torch
+
+    dh = torch.bmm(do, w2.transpose(1, 2).contiguous())
+    dw2 = torch.bmm(do.transpose(1, 2).contiguous(), h).transpose(1, 2).contiguous()
+    if activation == "silu":
+        s = torch.sigmoid(z)
+        dz = dh * (s + z * s * (1 - s))
+    elif activation == "sigmoid":
+        dz = dh * h * (1 - h)
+    elif activation == "leaky_relu":
+        dz = dh * torch.where(z > 0, 1.0, 0.01).to(dh.dtype)
+    else:
+        dz = dh
+    dx = torch.bmm(dz, w1.transpose(1, 2).contiguous())
+    dw1 = torch.bmm(x.transpose(1, 2).contiguous(), dz)
+    return dx, dw1, dw2
+
+
+def _device_used():
+    import torch
+
+    free, total = torch.cuda.mem_get_info()
+    return total - free
+
+
 def peak_memory(x, w1, w2, do, activation):
-    """Peak allocated MB of one fwd+bwd (example.py:142-200 method) for FlashMLP and for the
-    unfused PyTorch path that keeps Z and h from the forward (contiguous bmm operands)."""
+    """Peak allocated MB of one fwd+bwd (example.py:142-200 method) for FlashMLP (both backward
+    forms) and for the unfused PyTorch path, plus the device memory held outside torch's
+    allocator by the library (its code objects; fmlp_bwd_noalloc's static scratch is a code
+    object of its own, loaded at the first no-alloc call, measured last)."""
     import torch
 
     import flashmlp_amd as fm
+    from flashmlp_amd import _lib
 
     def flash():
         o = fm.flashmlp_fwd(x, w1, w2, activation)
@@ -160,28 +235,8 @@ def peak_memory(x, w1, w2, do, activation):
         return o, (lambda: fm.flashmlp_bwd(x, w1, w2, do, activation, recompute=True))
 
     def unfused():
-        z = torch.bmm(x, w1)
-        h = {"silu": torch.nn.functional.silu, "sigmoid": torch.sigmoid,
-             "leaky_relu": lambda t: torch.nn.functional.leaky_relu(t, 0.01)}.get(activation, lambda t: t)(z)
-        o = torch.bmm(h, w2)
-
-        def bwd():
-            dh = torch.bmm(do, w2.transpose(1, 2).contiguous())
-            dw2 = torch.bmm(h.transpose(1, 2).contiguous(), do)
-            if activation == "silu":
-                s = torch.sigmoid(z)
-                dz = dh * (s + z * s * (1 - s))
-            elif activation == "sigmoid":
-                dz = dh * h * (1 - h)
-            elif activation == "leaky_relu":
-                dz = dh * torch.where(z > 0, 1.0, 0.01).to(dh.dtype)
-            else:
-                dz = dh
-            dx = torch.bmm(dz, w1.transpose(1, 2).contiguous())
-            dw1 = torch.bmm(x.transpose(1, 2).contiguous(), dz)
-            return dx, dw1, dw2
-
-        return o, bwd
+        o, z, h = unfused_fwd(x, w1, w2, activation)
+        return o, (lambda: unfused_bwd(x, w1, w2, do, z, h, activation))
 
     out = {}
     for name, fn in (("flashmlp", flash), ("flashmlp_recompute", flash_recompute), ("pytorch_unfused", unfused)):
@@ -202,6 +257,27 @@ def peak_memory(x, w1, w2, do, activation):
         out[name] = {"fwd_alloc_mb": round(fwd_mb, 1), "peak_mb": round(peak_mb, 1)}
     out["peak_savings"] = round(1 - out["flashmlp"]["peak_mb"] / out["pytorch_unfused"]["peak_mb"], 4)
     out["peak_savings_recompute"] = round(1 - out["flashmlp_recompute"]["peak_mb"] / out["pytorch_unfused"]["peak_mb"], 4)
+
+    # fmlp_bwd_noalloc's static scratch: device memory taken by the first no-alloc call (no
+    # torch allocation happens in it), i.e. what a process using that entry point holds beyond
+    # the peaks above, which were measured before it was loaded
+    H, B, D = x.shape
+    E = w1.shape[2]
+    hs, bs = 1, min(B, 512)
+    xs, dos = x[:hs, :bs].contiguous(), do[:hs, :bs].contiguous()
+    w1s, w2s = w1[:hs].contiguous(), w2[:hs].contiguous()
+    gs = (torch.empty_like(xs), torch.empty_like(w1s), torch.empty_like(w2s))
+    code = {torch.bfloat16: _lib.FMLP_DTYPE_BF16, torch.float16: _lib.FMLP_DTYPE_F16}.get(x.dtype, _lib.FMLP_DTYPE_F32)
+    torch.cuda.synchronize()
+    used0 = _device_used()
+    p = lambda t: ctypes.c_void_p(t.data_ptr())
+    st = _lib.lib().fmlp_bwd_noalloc(p(xs), p(w1s), p(w2s), p(dos), *(p(t) for t in gs), hs, bs, D, E, code,
+                                     _lib.ACT_CODES[activation], ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(st, "backward (no allocation)")
+    torch.cuda.synchronize()
+    out["noalloc_scratch_device_mb"] = round((_device_used() - used0) / 2 ** 20, 1)
+    out["noalloc_scratch_note"] = ("held per device only by processes that call fmlp_bwd_noalloc (loaded at "
+                                   "its first call); not part of the peaks above")
     return out
 
 
@@ -250,6 +326,146 @@ def autograd_step_ms(x, w1, w2, do, act, warmup=3, iters=20):
     return _wall_ms(step, iters)
 
 
+def time_steps(fwd, bwd, steps, warmup):
+    """W untimed then K timed steps of fwd() then bwd() (bwd may be None): wall-clock ms per
+    step, and the mean fwd / bwd durations from HIP events on the current stream."""
+    import torch
+
+    for _ in range(warmup):
+        fwd()
+        if bwd is not None:
+            bwd()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    outs = None
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for k in range(steps):
+        ev[k][0].record()
+        o = fwd()
+        ev[k][1].record()
+        g = bwd() if bwd is not None else None
+        ev[k][2].record()
+        outs = (o, g)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / steps
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / steps if bwd is not None else 0.0
+    return wall, fwd_ms, bwd_ms, outs
+
+
+def _finite(outs):
+    import torch
+
+    o, g = outs
+    ok = bool(torch.isfinite(o.float()).all())
+    if g is not None:
+        ok = ok and all(bool(torch.isfinite(t.float()).all()) for t in g if t is not None)
+    return ok
+
+
+def _bwd_form(H, B, D, E, dt_name, act, accurate_dw=False, recompute=False):
+    from flashmlp_amd import _lib
+
+    code = {"bf16": _lib.FMLP_DTYPE_BF16, "f16": _lib.FMLP_DTYPE_F16, "f32": _lib.FMLP_DTYPE_F32}[dt_name]
+    if not _lib.lib().fmlp_shape_tuned(D, E, code):
+        return "generic"
+    code |= (_lib.FMLP_DW_HILO if accurate_dw else 0) | (_lib.FMLP_BWD_RECOMPUTE if recompute else 0)
+    return "stored-dZ" if _lib.lib().fmlp_bwd_stores_dz(H, B, D, E, code, _lib.ACT_CODES[act]) else "recompute"
+
+
+def _summary(H, B, D, E, dt_name, act, fwd_only, wall, fwd_ms, bwd_ms, bwd_form):
+    """Per-configuration figures: times, TFLOP/s (12u per step, 4u forward, 8u backward), % of
+    the dtype's dense MFMA peak, and algorithmic HBM GB/s of each call."""
+    u = float(H) * B * D * E
+    s = _es(dt_name)
+    peak = PEAK_TFLOPS[dt_name]
+    step_flops = (4 if fwd_only else 12) * u
+    r = {"H": H, "B": B, "D": D, "E": E, "dtype": dt_name, "activation": act or "linear",
+         "ms_per_step": round(wall, 4), "tflops": round(step_flops / (wall * 1e-3) / 1e12, 2),
+         "pct_of_peak": round(100 * step_flops / (wall * 1e-3) / 1e12 / peak, 2), "peak_tflops": peak,
+         "fwd_ms": round(fwd_ms, 4), "fwd_tflops": round(4 * u / (fwd_ms * 1e-3) / 1e12, 2),
+         "fwd_hbm_gbs": round((2 * H * B * D + 2 * H * D * E) * s / (fwd_ms * 1e-3) / 1e9, 1)}
+    if not fwd_only:
+        r.update({"bwd_ms": round(bwd_ms, 4), "bwd_tflops": round(8 * u / (bwd_ms * 1e-3) / 1e12, 2),
+                  "bwd_hbm_gbs": round((3 * H * B * D + 4 * H * D * E) * s / (bwd_ms * 1e-3) / 1e9, 1),
+                  "bwd_form": bwd_form})
+    return r
+
+
+def run_config(name, steps, warmup, **bwd_kw):
+    """One workload's step timed on freshly drawn inputs (the `configs` pass)."""
+    import torch
+
+    import flashmlp_amd as fm
+
+    H, B, D, E, dt_name, act, x_std, fwd_only = WORKLOADS[name]
+    x, w1, w2, do = make_gpu_inputs(H, B, D, E, _torch_dtype(dt_name), x_std)
+    fwd = lambda: fm.flashmlp_fwd(x, w1, w2, act)
+    bwd = None if fwd_only else (lambda: fm.flashmlp_bwd(x, w1, w2, do, act, **bwd_kw))
+    wall, f_ms, b_ms, outs = time_steps(fwd, bwd, steps, warmup)
+    r = _summary(H, B, D, E, dt_name, act, fwd_only, wall, f_ms, b_ms,
+                 None if fwd_only else _bwd_form(H, B, D, E, dt_name, act, **bwd_kw))
+    r["finite"] = _finite(outs)
+    if fwd_only:
+        r["note"] = "forward only (inference sweep)"
+    del x, w1, w2, do, outs
+    torch.cuda.empty_cache()
+    return r
+
+
+def vs_unfused(x4, w14, w24, do4, act4, steps, warmup):
+    """FlashMLP against the unfused PyTorch path on the same GPU and inputs: forward, and
+    forward + backward (direct calls for both, no autograd), at cfg4 and at performance.md's
+    shapes (bf16 SiLU, X~N(0,1/D) as example.py draws it, module init scales)."""
+    import torch
+
+    import flashmlp_amd as fm
+
+    def pair(x, w1, w2, do, act, k, w):
+        H, B, D = x.shape
+        E = w1.shape[2]
+        u = float(H) * B * D * E
+        f_fwd = lambda: fm.flashmlp_fwd(x, w1, w2, act)
+        f_bwd = lambda: fm.flashmlp_bwd(x, w1, w2, do, act)
+
+        def t_step():
+            o, z, h = unfused_fwd(x, w1, w2, act)
+            return unfused_bwd(x, w1, w2, do, z, h, act)
+
+        ff = time_steps(f_fwd, None, k, w)[0]
+        fb = time_steps(f_fwd, f_bwd, k, w)[0]
+        tf = time_steps(lambda: unfused_fwd(x, w1, w2, act)[0], None, k, w)[0]
+        for _ in range(w):
+            t_step()
+        tb = _wall_ms(t_step, k)
+        return {"H": H, "B": B, "D": D, "E": E, "flashmlp_fwd_ms": round(ff, 4),
+                "flashmlp_fwd_bwd_ms": round(fb, 4), "pytorch_fwd_ms": round(tf, 4),
+                "pytorch_fwd_bwd_ms": round(tb, 4), "speedup_fwd": round(tf / ff, 2),
+                "speedup_fwd_bwd": round(tb / fb, 2),
+                "flashmlp_fwd_bwd_tflops": round(12 * u / (fb * 1e-3) / 1e12, 1),
+                "pytorch_fwd_bwd_tflops": round(12 * u / (tb * 1e-3) / 1e12, 1)}
+
+    res = {"method": "wall clock of direct calls, W warmup then K steps, synchronised at both ends; unfused = "
+                     "bmm -> activation -> bmm keeping Z and h, backward as five bmm on contiguous operands "
+                     "(flashmlp.py:689-723)",
+           "cfg4": pair(x4, w14, w24, do4, act4, steps, warmup)}
+    rows = []
+    for H, B, D, E in EXAMPLE_SHAPES:
+        g = torch.Generator(device="cuda").manual_seed(0)
+        f = dict(device="cuda", dtype=torch.float32, generator=g)
+        x = (torch.randn(H, B, D, **f) / D ** 0.5).bfloat16()
+        w1 = (torch.randn(H, D, E, **f) / E ** 0.5).bfloat16()  # FlashMLP's init (flashmlp.py:586-591)
+        w2 = (torch.randn(H, E, D, **f) / D ** 0.5).bfloat16()
+        do = torch.randn(H, B, D, **f).bfloat16()
+        r = pair(x, w1, w2, do, "silu", 100, 10)
+        pub = EXAMPLE_PUBLISHED_MS[(H, B, D, E)]
+        r["reference_published_ms"] = {"triton_fwd": pub[0], "triton_fwd_bwd": pub[1], "hardware": "unstated"}
+        rows.append(r)
+    res["performance_md_shapes"] = rows
+    return res
+
+
 def run_example(args):
     """performance.md's four shapes through the FlashMLP module, timed like example.py
     (10 warmup + 100 iterations, wall clock, fwd = model(x), fwd+bwd = model(x).sum().backward())."""
@@ -291,8 +507,6 @@ def run_example(args):
 def run_mfma_ceiling(args):
     """Sustained executed bf16 MFMA rate with operands in registers (no memory traffic), random
     and all-zero operand bits: the power-limited ceiling the FlashMLP kernels are compared with."""
-    import ctypes
-
     import torch
 
     lib = ctypes.CDLL(os.path.join(ROOT, "flashmlp_amd", "libfmlp_ceiling.so"))
@@ -348,9 +562,12 @@ def main():
     ap.add_argument("--workload", default="cfg4", choices=sorted(WORKLOADS) + ["example", "mfma_ceiling"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-memory", action="store_true", help="skip the peak-memory comparison")
-    ap.add_argument("--no-extra", action="store_true", help="skip the autograd-step and host-overhead timings")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the autograd-step and host-overhead timings, the cfg4 forms, the configs pass "
+                         "and the unfused comparison (headline timing only)")
     ap.add_argument("--accurate-dw", action="store_true",
                     help="time the backward in its dW accuracy mode (h and dZ as hi + lo terms)")
+    ap.add_argument("--recompute", action="store_true", help="time the backward in its recompute-only form")
     ap.add_argument("--calib-copy-mb", type=int, default=0,
                     help="after timing, run device copies of this size (HBM counter calibration)")
     args = ap.parse_args()
@@ -379,36 +596,18 @@ def main():
     dtype = _torch_dtype(dt_name)
     x, w1, w2, do = make_gpu_inputs(H, B, D, E, dtype, x_std)
     torch.cuda.synchronize()
-    s = 2  # bytes per io element
+    s = _es(dt_name)
+    bwd_kw = dict(accurate_dw=args.accurate_dw, recompute=args.recompute)
 
-    for _ in range(args.warmup):
-        fm.flashmlp_fwd(x, w1, w2, act)
-        if not fwd_only:
-            fm.flashmlp_bwd(x, w1, w2, do, act, accurate_dw=args.accurate_dw)
-    torch.cuda.synchronize()
+    fwd = lambda: fm.flashmlp_fwd(x, w1, w2, act)
+    bwd = None if fwd_only else (lambda: fm.flashmlp_bwd(x, w1, w2, do, act, **bwd_kw))
+    ms_per_step, fwd_ms, bwd_ms, outs = time_steps(fwd, bwd, args.steps, args.warmup)
+    assert _finite(outs), "non-finite outputs"
+    del outs
 
     K = args.steps
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(K)]
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for k in range(K):
-        ev[k][0].record()
-        o = fm.flashmlp_fwd(x, w1, w2, act)
-        ev[k][1].record()
-        if not fwd_only:
-            g = fm.flashmlp_bwd(x, w1, w2, do, act, accurate_dw=args.accurate_dw)
-        ev[k][2].record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in ev) / K
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in ev) / K if not fwd_only else 0.0
-    assert torch.isfinite(o.float()).all()
-    if not fwd_only:
-        assert all(torch.isfinite(t.float()).all() for t in g)
-
     u = float(H) * B * D * E
     flops = (4 if fwd_only else 12) * u
-    ms_per_step = wall * 1e3 / K
     value = flops / (ms_per_step * 1e-3) / 1e12
     peak = PEAK_TFLOPS[dt_name]
     fwd_tf = 4 * u / (fwd_ms * 1e-3) / 1e12
@@ -427,6 +626,8 @@ def main():
     step_name = "fused MLP forward (inference sweep)" if fwd_only else "fused MLP fwd+bwd"
     if args.accurate_dw:
         step_name += " (dW accuracy mode)"
+    if args.recompute:
+        step_name += " (recompute-only backward)"
     line = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -449,7 +650,7 @@ def main():
     }
     if fwd_only:
         line["roofline"] = {
-            "kernel": "fmlp_fwd call: fmlp::fwd_kernel",
+            "kernel": "fmlp_fwd: fmlp::fwd_kernel",
             "bound": "mfma",
             "achieved": round(fwd_tf, 2),
             "peak": peak,
@@ -467,32 +668,43 @@ def main():
         line["bwd_ms"] = round(bwd_ms, 4)
         line["bwd_tflops"] = round(bwd_tf, 2)
         line["bwd_hbm_gbs"] = round(bwd_bytes / (bwd_ms * 1e-3) / 1e9, 1)
-        from flashmlp_amd import _lib
-        code = (_lib.FMLP_DTYPE_BF16 if dt_name == "bf16" else _lib.FMLP_DTYPE_F16) | \
-            (_lib.FMLP_DW_HILO if args.accurate_dw else 0)
-        stores_dz = bool(_lib.lib().fmlp_bwd_stores_dz(H, B, D, E, code, _lib.ACT_CODES[act]))
-        line["bwd_form"] = "stored-dZ" if stores_dz else "recompute"
+        form = _bwd_form(H, B, D, E, dt_name, act, **bwd_kw)
+        line["bwd_form"] = form
+        kernels = {"stored-dZ": "fmlp::dw2_kernel (storing dZ), fmlp::dxg_kernel",
+                   "recompute": "fmlp::bwd_kernel (dW and dX programs)",
+                   "generic": "fmlp::gen_dw_kernel, fmlp::gen_dx_kernel"}[form]
         line["roofline"] = {
-            "kernel": ("fmlp_bwd call, stored-dZ form: fmlp::dw2_kernel (dW programs, also writing dZ), "
-                       "fmlp::dw_reduce_kernel when they split B, then fmlp::dxg_kernel (dX = dZ W1^T)"
-                       if stores_dz else
-                       "fmlp_bwd call, recompute form: fmlp::bwd_kernel (dW and dX programs in one launch; "
-                       "then fmlp::dw_reduce_kernel when the dW programs split B)"),
+            "kernel": f"fmlp_bwd ({form}): {kernels}",
             "bound": "mfma",
             "achieved": round(bwd_tf, 2),
             "peak": peak,
             "unit": "TFLOP/s",
             "frac": round(bwd_tf / peak, 4),
-            "traffic": traffic_from_profile("bwd", args.workload),
+            "traffic": traffic_from_profile("bwd", args.workload) if not (args.accurate_dw or args.recompute) else None,
             "algorithmic_flops_per_launch": 8 * u,
             "algorithmic_bytes_per_launch": bwd_bytes,
             "avg_launch_ms": round(bwd_ms, 4),
         }
     if not args.no_extra:
-        line["host_us_per_call"] = {"fwd": round(host_us_per_call(lambda: fm.flashmlp_fwd(x, w1, w2, act)), 2)}
+        line["host_us_per_call"] = {"fwd": round(host_us_per_call(fwd), 2)}
         if not fwd_only:
-            line["host_us_per_call"]["bwd"] = round(host_us_per_call(lambda: fm.flashmlp_bwd(x, w1, w2, do, act)), 2)
+            line["host_us_per_call"]["bwd"] = round(host_us_per_call(bwd), 2)
             line["autograd_ms_per_step"] = round(autograd_step_ms(x, w1, w2, do, act), 4)
+        if args.workload == "cfg4" and not (args.accurate_dw or args.recompute):
+            # the same step in the north star's recompute-only form and in the dW accuracy mode
+            forms = {}
+            for name, kw in (("recompute", dict(recompute=True)), ("accurate_dw", dict(accurate_dw=True)),
+                             ("recompute_accurate_dw", dict(recompute=True, accurate_dw=True))):
+                wall, f_ms, b_ms, o = time_steps(fwd, lambda: fm.flashmlp_bwd(x, w1, w2, do, act, **kw),
+                                                 K, max(3, min(args.warmup, 5)))
+                r = _summary(H, B, D, E, dt_name, act, False, wall, f_ms, b_ms, _bwd_form(H, B, D, E, dt_name, act, **kw))
+                forms[name] = {k: r[k] for k in ("ms_per_step", "tflops", "pct_of_peak", "fwd_ms", "bwd_ms",
+                                                 "bwd_tflops", "bwd_form")}
+                forms[name]["finite"] = _finite(o)
+                del o
+            line["cfg4_forms"] = forms
+            line["configs"] = {name: run_config(name, 10, 3) for name in CONFIG_PASS}
+            line["vs_pytorch_unfused"] = vs_unfused(x, w1, w2, do, act, 10, 3)
     if not args.no_memory and not fwd_only:
         line["memory"] = peak_memory(x, w1, w2, do, act)
     if not args.no_cpu:

@@ -21,7 +21,7 @@ ROOT = PKG.parent
 CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIB = PKG / "libflashmlp.so"
-SOURCES = ["fmlp_fwd.hip", "fmlp_bwd.hip", "fmlp_gen.hip", "fmlp_abi.cpp"]
+SOURCES = ["fmlp_fwd.hip", "fmlp_bwd.hip", "fmlp_gen.hip", "fmlp_scratch.hip", "fmlp_abi.cpp"]
 CEILING_SRC = "fmlp_ceiling.hip"
 CEILING_LIB = PKG / "libfmlp_ceiling.so"
 ARCH = os.environ.get("FLASHMLP_ARCH", "gfx950")

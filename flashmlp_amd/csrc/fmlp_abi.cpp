@@ -273,6 +273,7 @@ FMLP_EXPORT int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, 
 FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   if (check_shape(H, B, D, E, dtype) != FMLP_OK) return 0;
   if (!tuned_shape(D, E, io_of(dtype))) return 0;  // the generic kernels need no workspace
+  if (dtype & FMLP_BWD_NO_DW) return 0;            // the dX programs alone use no workspace
   int cus = 0;
   if (num_cus_current(&cus) != FMLP_OK) return 0;
   // the plan depends on the activation, which this query does not take: the largest over them
@@ -326,21 +327,20 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
   if (dense && aligned && tuned_shape(D, E, io)) {
     int cus = 0;
     if ((st = num_cus_current(&cus))) return st;
+    // with a scratch limit the plan only considers B splits (and the stored-dZ form) whose
+    // workspace fits it; the unsplit recompute form needs none, so a plan always exists
     const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus,
                                               noalloc ? fmlp::kScratchBytes : (size_t)-1);
-    void* ws = workspace;
-    if (plan.ws_bytes > 0) {
+    // the dX programs alone (FMLP_BWD_NO_DW) touch no workspace
+    const size_t ws_need = want_dw ? plan.ws_bytes : 0;
+    void* ws = want_dw ? workspace : nullptr;
+    if (ws_need > 0) {
       if (noalloc) {
-        if (plan.ws_bytes > fmlp::kScratchBytes)
-          return fail(FMLP_ERR_WORKSPACE,
-                      "fmlp_bwd_noalloc: these shapes need %zu bytes of scratch, the static scratch holds %zu "
-                      "(FMLP_SCRATCH_MAX_BYTES); call fmlp_bwd with a workspace instead",
-                      plan.ws_bytes, fmlp::kScratchBytes);
         e = fmlp::scratch_current_device(&ws);
         if (e != hipSuccess) return fail(FMLP_ERR_HIP, "scratch lookup: %s", hipGetErrorString(e));
       } else {
-        if (workspace == nullptr || workspace_bytes < plan.ws_bytes)
-          return fail(FMLP_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, plan.ws_bytes);
+        if (workspace == nullptr || workspace_bytes < ws_need)
+          return fail(FMLP_ERR_WORKSPACE, "workspace of %zu bytes given, %zu needed", workspace_bytes, ws_need);
         if (!aligned16(workspace)) return fail(FMLP_ERR_INVALID_ARG, "workspace is not 16-byte aligned");
       }
     }

@@ -1196,36 +1196,6 @@ static hipError_t launch_bwd_a(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   }
 }
 
-// ------------------------------------------------------------------------------------
-// Static scratch for fmlp_bwd_noalloc: the dW programs' fp32 partials (the workspace
-// fmlp_bwd takes from its caller) live in this file-scope device array instead. Each device
-// that loads the library holds its own copy until the process ends. Every call on a device
-// shares that device's copy, so calls that overlap on one device race. The partial layout
-// is fully written by the dW programs before dw_reduce_kernel reads it: nothing in it has
-// to start at zero.
-// ------------------------------------------------------------------------------------
-static __device__ __align__(256) unsigned char scratch[kScratchBytes];
-
-hipError_t scratch_current_device(void** ptr) {
-  constexpr int kDevices = 64;
-  static std::mutex mu;
-  static void* addr[kDevices] = {};
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= kDevices) return hipErrorInvalidDevice;
-  std::lock_guard<std::mutex> lock(mu);
-  if (addr[dev] == nullptr) {
-    // the host-side name `scratch` is not a device address: only this lookup yields one
-    void* p = nullptr;
-    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    if (e != hipSuccess) return e;
-    addr[dev] = p;
-  }
-  *ptr = addr[dev];
-  return hipSuccess;
-}
-
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
   if (a.bf16) {
     if (a.D == 128) return launch_bwd_a<true, 128>(a, p, st);

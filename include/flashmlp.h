@@ -16,10 +16,14 @@
  * The library never allocates: the caller passes every buffer, including the backward
  * workspace.
  *
- * Calls are asynchronous on the given hipStream_t (NULL = default stream), never
- * synchronise, keep no mutable global state and are reentrant. A non-zero return is one
- * of fmlp_status; fmlp_status_string() names it and fmlp_last_error() (thread-local) says
- * which argument was rejected.
+ * Calls are asynchronous on the given hipStream_t (NULL = default stream) and never
+ * synchronise. The library's only global state is caches of values that never change for a
+ * device and shape (CU counts, backward plans, each behind its own lock), the thread-local
+ * error string, and fmlp_bwd_noalloc's per-device scratch: every entry point but
+ * fmlp_bwd_noalloc is reentrant and may run concurrently on any streams and threads;
+ * fmlp_bwd_noalloc calls that overlap on one device race (see there). A non-zero return is
+ * one of fmlp_status; fmlp_status_string() names it and fmlp_last_error() (thread-local)
+ * says which argument was rejected.
  */
 #ifndef FLASHMLP_H_
 #define FLASHMLP_H_
@@ -76,8 +80,9 @@ typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1, FMLP_DTYPE_F32 = 2 } fml
 /* OR-ed into the dtype argument of fmlp_bwd / fmlp_bwd_strided / fmlp_bwd_noalloc: the caller
  * needs no dx (FMLP_BWD_NO_DX: dx may be NULL and is not written; only the dW programs run, in
  * the recompute form's plan) or no dw1, dw2 (FMLP_BWD_NO_DW: both may be NULL and are not
- * written; only the dX programs run). The results that are computed are bit-identical to the
- * recompute form's (FMLP_BWD_RECOMPUTE). No counterpart in the reference, whose backward
+ * written; only the dX programs run, with no workspace: fmlp_bwd_workspace_bytes is 0 and
+ * `workspace` may be NULL). The results that are computed are bit-identical to the recompute
+ * form's (FMLP_BWD_RECOMPUTE) of the same entry point. No counterpart in the reference, whose backward
  * always computes all three: for autograd callers whose input, or whose weights, need no
  * gradient. Both flags together: nothing to compute. */
 #define FMLP_BWD_NO_DX 0x1000
@@ -126,9 +131,10 @@ int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int
                      int64_t E, const int64_t* x_strides, const int64_t* w1_strides, const int64_t* w2_strides,
                      int dtype, int act, void* stream);
 
-/* Bytes of device workspace fmlp_bwd needs for these shapes and dtype flags (FMLP_DW_HILO and
- * FMLP_BWD_RECOMPUTE change it) on the current device, whatever the activation (0 when none is
- * needed). */
+/* Bytes of device workspace fmlp_bwd / fmlp_bwd_strided need for these shapes and dtype flags
+ * on the current device, whatever the activation (0 when none is needed). Every backward flag
+ * can change it (FMLP_DW_HILO, FMLP_BWD_RECOMPUTE, FMLP_BWD_STORE_DZ and FMLP_BWD_NO_DX change
+ * the plan; with FMLP_BWD_NO_DW it is 0): query it with the flags of the call it is for. */
 size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
 /* 1 when fmlp_bwd takes the stored-dZ form for these shapes, dtype flags and activation on the
@@ -162,15 +168,17 @@ int fmlp_bwd_strided(const void* x, const void* w1, const void* w2, const void* 
 
 /*
  * Backward without allocation: fmlp_bwd with the workspace replaced by the library's own
- * static device scratch (FMLP_SCRATCH_MAX_BYTES per device, held from the first call on a
- * device until the process ends). No counterpart in the reference: for callers that cannot
- * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
- * forbid hipMalloc). It calls no hipMalloc, hipFree or allocating routine. It only takes the
- * forms whose workspace fits the scratch (the stored-dZ form only when dZ fits); shapes whose
- * recompute-only workspace (fmlp_bwd_workspace_bytes with FMLP_BWD_RECOMPUTE) exceeds
- * FMLP_SCRATCH_MAX_BYTES return FMLP_ERR_WORKSPACE. All calls on one device share that
- * device's scratch: calls that overlap on one device (other streams, other threads) race;
- * serialise them.
+ * static device scratch (FMLP_SCRATCH_MAX_BYTES per device, in a code object of its own that is
+ * loaded onto a device, and so reserved there, at the first fmlp_bwd_noalloc call on it, until
+ * the process ends; processes that never call it do not hold it). No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). It calls no hipMalloc, hipFree or
+ * allocating routine. Its plan only considers B splits of the dW programs, and the stored-dZ
+ * form, whose workspace fits the scratch: where fmlp_bwd would split B more finely (or store
+ * dZ) than the scratch allows, it takes a smaller split (or the recompute form) instead of
+ * failing, so its dW results can differ from fmlp_bwd's in the last bits (summation order)
+ * and it is never FMLP_ERR_WORKSPACE. All calls on one device share that device's scratch:
+ * calls that overlap on one device (other streams, other threads) race; serialise them.
  */
 #define FMLP_SCRATCH_MAX_BYTES ((size_t)64 << 20)
 int fmlp_bwd_noalloc(const void* x, const void* w1, const void* w2, const void* dout, void* dx, void* dw1, void* dw2,

@@ -1,8 +1,12 @@
-"""Blockwise restatement of the reference backward programs (test infrastructure only).
+"""Blockwise restatement of the reference kernels (test infrastructure only).
 
-Follows the loop structure of the reference's two backward roles literally, one tile at a
-time, with fp32 accumulation and `.to(io)` exactly where the reference casts:
+Follows the loop structure of the reference's forward program and its two backward roles
+literally, one tile at a time, with fp32 accumulation and `.to(io)` exactly where the
+reference casts:
 
+  forward  flashmlp.py:63-158    per B-block, loop over E-blocks:
+           z = x @ w1 (fp32) :137; h = act(z).to(io) :140-147; o += h @ w2 (fp32) :150;
+           o.to(io) at the store :157
   dX role  flashmlp.py:165-244   per B-block, loop over E-blocks:
            z = x @ w1 (fp32) :212; h = act(z).to(io) :214-221; dh = do @ w2^T (fp32) :224;
            dz = (dh * act'(z, h)).to(io) :227-235; dx += dz @ w1^T (fp32) :238
@@ -50,6 +54,24 @@ def _dz(z, h_io, dh, activation, deriv):
         sig = h_io if deriv == "reference" else torch.sigmoid(z)
         return dh * sig * (1 - sig)  # flashmlp.py:231-233
     return dh
+
+
+def fwd_blocks(x, w1, w2, activation="", io_dtype=torch.bfloat16, block_b=64, block_e=64, round_out=True):
+    """o as an fp32 tensor, computed tile by tile like the reference's forward program."""
+    x, w1, w2 = (t.detach().to("cpu", torch.float32) for t in (x, w1, w2))
+    H, B, D = x.shape
+    E = w1.shape[2]
+    o = torch.zeros(H, B, D)
+    for h in range(H):
+        for b0 in range(0, B, block_b):  # one program per B-block (flashmlp.py:82-85)
+            xb = x[h, b0:b0 + block_b]
+            acc = torch.zeros(xb.shape[0], D)
+            for e0 in range(0, E, block_e):  # flashmlp.py:130-154
+                z = xb @ w1[h, :, e0:e0 + block_e]
+                h_io = _act(z, activation).to(io_dtype).to(torch.float32)
+                acc += h_io @ w2[h, e0:e0 + block_e]
+            o[h, b0:b0 + block_b] = acc
+    return o.to(io_dtype).to(torch.float32) if round_out else o
 
 
 def bwd_blocks(x, w1, w2, do, activation="", io_dtype=torch.bfloat16, block_b=64, block_e=64,

@@ -36,14 +36,14 @@ def _normrel(a, b):
     return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
 
 
-def _check(name, H, B, D, E, dtype, act, x_std=1.0, seed=0, heads=None, rel_bound=1e-4):
+def _check(name, H, B, D, E, dtype, act, x_std=1.0, seed=0, heads=None, rel_bound=1e-4, recompute=False):
     import flashmlp_amd as fm
 
     x, w1, w2, do = make_inputs(H, B, D, E, dtype, x_std, seed)
-    _say(f"[accurate_dw] {name}: H={H} B={B} D={D} E={E} {dtype} act='{act}' seed={seed}")
+    _say(f"[accurate_dw] {name}: H={H} B={B} D={D} E={E} {dtype} act='{act}' seed={seed} recompute={recompute}")
     xd, w1d, w2d, dod = (t.cuda() for t in (x, w1, w2, do))
-    dx, dw1, dw2 = fm.flashmlp_bwd(xd, w1d, w2d, dod, act, accurate_dw=True)
-    dx0, dw10, dw20 = fm.flashmlp_bwd(xd, w1d, w2d, dod, act)
+    dx, dw1, dw2 = fm.flashmlp_bwd(xd, w1d, w2d, dod, act, accurate_dw=True, recompute=recompute)
+    dx0, dw10, dw20 = fm.flashmlp_bwd(xd, w1d, w2d, dod, act, recompute=recompute)
     torch.cuda.synchronize()
     assert torch.equal(dx, dx0), "dX must not depend on the dW mode"
     hs = list(range(H)) if heads is None else heads
@@ -79,9 +79,12 @@ def test_config3():
     _check("cfg3", c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=[0, c.H - 1], rel_bound=5e-3)
 
 
-def test_config4_north_star():
+@pytest.mark.parametrize("recompute", [False, True], ids=["plan-form", "recompute-form"])
+def test_config4_north_star(recompute):
+    # the plan's form (stored dZ at this shape) and the reference's recompute-only form
     c = CONFIGS["cfg4"]
-    res = _check("cfg4", c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=[0, 17, 31], rel_bound=5e-3)
+    res = _check("cfg4", c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=[0, 17, 31], rel_bound=5e-3,
+                 recompute=recompute)
     _say(f"[accurate_dw] cfg4 dW elementwise-3e-2 misses vs fp32: dW1 {res['dw1_fail']:.4f} dW2 {res['dw2_fail']:.4f}"
          f" (default mode normwise {res['dw1_rel_default']:.2e} / {res['dw2_rel_default']:.2e})")
 

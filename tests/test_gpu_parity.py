@@ -51,14 +51,14 @@ def _gpu():
     return flashmlp_amd
 
 
-def run_case(name, H, B, D, E, dtype, act, x_std=1.0, seed=0, heads=None, check_bwd=True):
+def run_case(name, H, B, D, E, dtype, act, x_std=1.0, seed=0, heads=None, check_bwd=True, bwd_kw=None):
     fm = _gpu()
     x, w1, w2, do = make_inputs(H, B, D, E, dtype, x_std, seed)
-    _say(f"[parity] {name}: H={H} B={B} D={D} E={E} {dtype} act='{act}' seed={seed}")
+    _say(f"[parity] {name}: H={H} B={B} D={D} E={E} {dtype} act='{act}' seed={seed} bwd={bwd_kw or {}}")
     xd, w1d, w2d, dod = (t.cuda() for t in (x, w1, w2, do))
     o = fm.flashmlp_fwd(xd, w1d, w2d, act)
     if check_bwd:
-        dx, dw1, dw2 = fm.flashmlp_bwd(xd, w1d, w2d, dod, act)
+        dx, dw1, dw2 = fm.flashmlp_bwd(xd, w1d, w2d, dod, act, **(bwd_kw or {}))
     torch.cuda.synchronize()
     hs = list(range(H)) if heads is None else heads
     sel = lambda t: t[hs].cpu()
@@ -145,6 +145,21 @@ def test_config4_north_star():
     res = run_case("cfg4", c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=[0, 17, 31])
     _say(f"[parity] cfg4 dW elementwise-3e-2 fraction vs fp32 oracle: dW1 {res['dw1_fail_vs_fp32']:.4f} "
          f"dW2 {res['dw2_fail_vs_fp32']:.4f}")
+    b1, b2 = DW_FP32_MISS_BOUND["cfg4"]
+    assert res["dw1_fail_vs_fp32"] <= b1 and res["dw2_fail_vs_fp32"] <= b2, res
+
+
+def test_config4_recompute_form():
+    """cfg4 in the reference's recompute-only backward (flashmlp.py:341-421: the dX programs
+    recompute Z and dH, no dZ is stored), the form the north star names; the plan picks the
+    stored-dZ form at this shape, so it is forced here. Same heads and bars as above."""
+    from flashmlp_amd import _lib
+
+    c = CONFIGS["cfg4"]
+    code = _lib.FMLP_DTYPE_BF16 | _lib.FMLP_BWD_RECOMPUTE
+    assert _lib.lib().fmlp_bwd_stores_dz(c.H, c.B, c.D, c.E, code, _lib.ACT_CODES[c.activation]) == 0
+    res = run_case("cfg4-recompute", c.H, c.B, c.D, c.E, c.dtype, c.activation, c.x_std, heads=[0, 17, 31],
+                   bwd_kw=dict(recompute=True))
     b1, b2 = DW_FP32_MISS_BOUND["cfg4"]
     assert res["dw1_fail_vs_fp32"] <= b1 and res["dw2_fail_vs_fp32"] <= b2, res
 

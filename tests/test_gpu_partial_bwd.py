@@ -1,0 +1,154 @@
+"""Partial backward (FMLP_BWD_NO_DX / FMLP_BWD_NO_DW) through every backward entry point of
+the C ABI: fmlp_bwd, fmlp_bwd_strided (dense strides: tuned kernels; a strided view: generic
+kernels) and fmlp_bwd_noalloc.
+
+For each entry point and flag:
+  * the unwanted outputs are passed filled with a sentinel byte pattern and must come back
+    unchanged (the header promises they are not written);
+  * the wanted outputs are passed filled with NaN bytes and must come back NaN-free and
+    bit-identical to the same entry point's full backward in the recompute form
+    (FMLP_BWD_RECOMPUTE), which the partial backward runs the programs of;
+  * with FMLP_BWD_NO_DW no workspace is needed: fmlp_bwd_workspace_bytes is 0 and a NULL
+    workspace is accepted, on a shape whose dW programs split B (where the full backward does
+    need one).
+No counterpart in the reference, whose backward always computes all three gradients.
+"""
+import ctypes
+import sys
+
+import pytest
+import torch
+
+from flashmlp_amd import _lib
+from oracle.inputs import make_inputs
+
+pytestmark = pytest.mark.gpu
+
+_DT = {torch.float16: _lib.FMLP_DTYPE_F16, torch.bfloat16: _lib.FMLP_DTYPE_BF16}
+SENTINEL = 0x5A  # 0x5A5A: a finite fp16 / bf16 value no gradient here takes
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _filled(shape, dtype, byte):
+    t = torch.empty(shape, dtype=dtype, device="cuda")
+    t.view(torch.uint8).fill_(byte)
+    return t
+
+
+def _strides(t):
+    return (ctypes.c_int64 * 3)(*t.stride())
+
+
+def _call(entry, x, w1, w2, do, act, flags, outs, ws=None, ws_bytes=0):
+    L = _lib.lib()
+    H, B, D = x.shape
+    E = w1.shape[2]
+    code = _DT[x.dtype] | flags
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dx, dw1, dw2 = outs
+    if entry == "fmlp_bwd":
+        st = L.fmlp_bwd(_p(x), _p(w1), _p(w2), _p(do), _p(dx), _p(dw1), _p(dw2), H, B, D, E, code,
+                        _lib.ACT_CODES[act], _p(ws), ws_bytes, stream)
+    elif entry == "fmlp_bwd_strided":
+        st = L.fmlp_bwd_strided(_p(x), _p(w1), _p(w2), _p(do), _p(dx), _p(dw1), _p(dw2), H, B, D, E,
+                                _strides(x), _strides(w1), _strides(w2), _strides(do), code,
+                                _lib.ACT_CODES[act], _p(ws), ws_bytes, stream)
+    else:
+        st = L.fmlp_bwd_noalloc(_p(x), _p(w1), _p(w2), _p(do), _p(dx), _p(dw1), _p(dw2), H, B, D, E, code,
+                                _lib.ACT_CODES[act], stream)
+    _lib.check(st, f"{entry} flags={flags:#x}")
+    torch.cuda.synchronize()
+
+
+def _workspace(entry, x, w1, flags):
+    """(tensor or None, bytes) the entry point needs for these flags (none for no-alloc)."""
+    if entry == "fmlp_bwd_noalloc":
+        return None, 0
+    H, B, D = x.shape
+    E = w1.shape[2]
+    n = _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, _DT[x.dtype] | flags)
+    return (torch.empty(n, dtype=torch.uint8, device="cuda") if n else None), n
+
+
+CASES = [
+    # H, B, D, E, dtype, act, seed, x transposed (a strided view: generic kernels)
+    (2, 4096, 128, 512, torch.bfloat16, "silu", 71, False),      # tuned kernels, B split
+    (8, 4097, 64, 2048, torch.float16, "sigmoid", 72, False),    # tuned kernels, tails
+    (3, 300, 32, 45, torch.float16, "leaky_relu", 73, False),    # generic kernels (D = 32)
+    (2, 260, 64, 136, torch.bfloat16, "silu", 74, True),         # generic kernels (strided X)
+]
+ENTRIES = ["fmlp_bwd", "fmlp_bwd_strided", "fmlp_bwd_noalloc"]
+
+
+@pytest.mark.parametrize("entry", ENTRIES)
+@pytest.mark.parametrize("H,B,D,E,dt,act,seed,xt", CASES,
+                         ids=["bf16-D128-split", "fp16-D64-tail", "fp16-D32-generic", "bf16-D64-stridedX"])
+def test_partial_backward_writes_only_what_is_asked(entry, H, B, D, E, dt, act, seed, xt):
+    if xt and entry != "fmlp_bwd_strided":
+        pytest.skip("a strided view goes through fmlp_bwd_strided only")
+    x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=seed))
+    if xt:  # same values, X stored as (H, D, B) and viewed as (H, B, D)
+        x = x.transpose(1, 2).contiguous().transpose(1, 2)
+    _say(f"[partial] {entry} H={H} B={B} D={D} E={E} {dt} act='{act}' strided_x={xt}")
+    ws, n = _workspace(entry, x, w1, _lib.FMLP_BWD_RECOMPUTE)
+    full = tuple(_filled(s, dt, 0xFF) for s in ((H, B, D), (H, D, E), (H, E, D)))
+    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_RECOMPUTE, full, ws, n)
+    for name, t in zip(("dx", "dw1", "dw2"), full):
+        assert not torch.isnan(t).any(), f"full backward left {name} elements unwritten"
+
+    # dW only: dx is a sentinel-filled buffer that must stay untouched
+    ws, n = _workspace(entry, x, w1, _lib.FMLP_BWD_NO_DX)
+    dx_s = _filled((H, B, D), dt, SENTINEL)
+    dw1, dw2 = _filled((H, D, E), dt, 0xFF), _filled((H, E, D), dt, 0xFF)
+    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DX, (dx_s, dw1, dw2), ws, n)
+    assert bool((dx_s.view(torch.uint8) == SENTINEL).all()), "FMLP_BWD_NO_DX wrote dx"
+    assert torch.equal(dw1, full[1]) and torch.equal(dw2, full[2])
+
+    # dX only: dw1, dw2 are sentinel-filled and must stay untouched; no workspace at all
+    if entry != "fmlp_bwd_noalloc":
+        assert _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, _DT[dt] | _lib.FMLP_BWD_NO_DW) == 0
+    dx = _filled((H, B, D), dt, 0xFF)
+    dw1_s, dw2_s = _filled((H, D, E), dt, SENTINEL), _filled((H, E, D), dt, SENTINEL)
+    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DW, (dx, dw1_s, dw2_s), None, 0)
+    assert bool((dw1_s.view(torch.uint8) == SENTINEL).all()), "FMLP_BWD_NO_DW wrote dw1"
+    assert bool((dw2_s.view(torch.uint8) == SENTINEL).all()), "FMLP_BWD_NO_DW wrote dw2"
+    assert torch.equal(dx, full[0])
+
+    # NULL for the outputs nobody asked for
+    dw1, dw2 = _filled((H, D, E), dt, 0xFF), _filled((H, E, D), dt, 0xFF)
+    ws, n = _workspace(entry, x, w1, _lib.FMLP_BWD_NO_DX)
+    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DX, (None, dw1, dw2), ws, n)
+    assert torch.equal(dw1, full[1]) and torch.equal(dw2, full[2])
+    dx = _filled((H, B, D), dt, 0xFF)
+    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DW, (dx, None, None), None, 0)
+    assert torch.equal(dx, full[0])
+
+
+def test_no_dw_needs_no_workspace_where_the_full_backward_does():
+    H, B, D, E, dt = 2, 4096, 128, 512, torch.bfloat16
+    code = _DT[dt] | _lib.FMLP_BWD_RECOMPUTE
+    need = _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, code)
+    _say(f"[partial] workspace full={need} no_dw={_lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, code | _lib.FMLP_BWD_NO_DW)}")
+    assert need > 0, "this shape should split B in the recompute form"
+    assert _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, code | _lib.FMLP_BWD_NO_DW) == 0
+    # the full backward refuses a NULL workspace here; the dX-only one takes it
+    x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=75))
+    outs = tuple(torch.empty(s, dtype=dt, device="cuda") for s in ((H, B, D), (H, D, E), (H, E, D)))
+    L = _lib.lib()
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    st = L.fmlp_bwd(_p(x), _p(w1), _p(w2), _p(do), *(_p(t) for t in outs), H, B, D, E, code,
+                    _lib.ACT_CODES["silu"], None, 0, stream)
+    assert st == 4, "the full backward must report FMLP_ERR_WORKSPACE without its workspace"
+    st = L.fmlp_bwd(_p(x), _p(w1), _p(w2), _p(do), _p(outs[0]), None, None, H, B, D, E,
+                    code | _lib.FMLP_BWD_NO_DW, _lib.ACT_CODES["silu"], None, 0, stream)
+    assert st == 0, _lib.lib().fmlp_last_error().decode()
+    torch.cuda.synchronize()
+    assert not torch.isnan(outs[0]).any()

@@ -145,6 +145,43 @@ def test_emulation_reduces_to_restatement_in_fp32(act):
         torch.testing.assert_close(a, b, rtol=2e-5, atol=2e-5)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16], ids=["bf16", "f16"])
+@pytest.mark.parametrize("act", ACTS)
+def test_emu_fwd_matches_blockwise_program(act, dt):
+    # emu_fwd against the tile-by-tile restatement of the reference's forward program
+    # (flashmlp.py:130-157): same cast points, different summation order
+    from oracle import blockwise
+
+    x, w1, w2, _ = make_inputs(2, 200, 64, 320, dt, x_std=2.0 if act == "sigmoid" else 1.0, seed=13, with_do=False)
+    e = emulate.emu_fwd(x, w1, w2, act, dt, round_out=False)
+    b = blockwise.fwd_blocks(x, w1, w2, act, dt, round_out=False)
+    assert _rel(e, b) < 2e-5
+
+
+@pytest.mark.parametrize("act", ["silu", "sigmoid", "leaky_relu"])
+def test_planted_fwd_cast_positions_are_detected(act):
+    # the forward rounds h = act(z) to the io dtype, not z before the activation and not only
+    # o at the end: each planted position moves o far beyond the fp32 noise that separates
+    # emu_fwd from the blockwise program (leaky_relu commutes with the rounding of z, so only
+    # the missing cast is observable there)
+    from oracle import blockwise
+
+    dt = torch.bfloat16
+    x, w1, w2, _ = make_inputs(2, 256, 64, 256, dt, seed=14, with_do=False)
+    ref = blockwise.fwd_blocks(x, w1, w2, act, dt, round_out=False)
+    assert _rel(emulate.emu_fwd(x, w1, w2, act, dt, round_out=False), ref) < 2e-5
+    xs, a, b = (t.float() for t in (x, w1, w2))
+    z = torch.bmm(xs, a)
+    q = lambda t: t.to(dt).float()
+    z_first = torch.bmm(q(emulate._h(q(z), act)), b)   # z rounded before the activation too
+    z_only = torch.bmm(emulate._h(q(z), act), b)       # z rounded instead of h
+    no_cast = torch.bmm(emulate._h(z, act), b)         # h kept in fp32
+    assert _rel(no_cast, ref) > 5e-4
+    if act != "leaky_relu":
+        assert _rel(z_first, ref) > 5e-4
+        assert _rel(z_only, ref) > 5e-4
+
+
 def test_emulation_cast_point_is_observable():
     # the emulation rounds h to the io dtype before the second product; a planted variant
     # without that cast must differ from it by more than the fp32 summation noise
