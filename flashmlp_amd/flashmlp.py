@@ -94,6 +94,46 @@ def _tuned(D: int, E: int, dtype: int) -> bool:
     return bool(_lib.lib().fmlp_shape_tuned(D, E, dtype))
 
 
+# torch's current HIP stream of a device, as the raw handle the C ABI takes, and the current
+# device: the private accessors skip building a torch.cuda.Stream object (about 2 us per call)
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_get_device = getattr(torch._C, "_cuda_getDevice", None)
+
+
+def _stream_of(index: int) -> int:
+    if _raw_stream is not None:
+        return _raw_stream(index)
+    return torch.cuda.current_stream(index).cuda_stream
+
+
+class _OnDevice:
+    """Makes `index` the current device for the C ABI call (the library launches on the current
+    device) only when it is not already; restores the previous one afterwards."""
+
+    __slots__ = ("index", "prev")
+
+    def __init__(self, index: int):
+        self.index = index
+        self.prev = None
+
+    def __enter__(self):
+        cur = _get_device() if _get_device is not None else torch.cuda.current_device()
+        if cur != self.index:
+            self.prev = cur
+            torch.cuda.set_device(self.index)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev is not None:
+            torch.cuda.set_device(self.prev)
+        return False
+
+
+def _index(t: torch.Tensor) -> int:
+    i = t.device.index
+    return i if i is not None else torch.cuda.current_device()
+
+
 def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation: str = "") -> torch.Tensor:
     """FlashMLP forward pass (reference: flashmlp.py:428-477).
 
@@ -103,20 +143,21 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
     Returns:
         O = act(x @ w1) @ w2 of shape (H, B, D), dtype of x.
     """
-    assert x.shape[0] == w1.shape[0], "Number of heads must match"
-    assert x.shape[0] == w2.shape[0], "Number of heads must match"
-    assert x.shape[2] == w1.shape[1], "Hidden dimension mismatch"
-    assert w1.shape[2] == w2.shape[1], "Intermediate dimension mismatch"
-    assert x.shape[2] == w2.shape[2], "Output dimension mismatch"
-
     H, B, D = x.shape
-    E = w1.shape[2]
+    H1, D1, E = w1.shape
+    H2, E2, D2 = w2.shape
+    assert H == H1, "Number of heads must match"
+    assert H == H2, "Number of heads must match"
+    assert D == D1, "Hidden dimension mismatch"
+    assert E == E2, "Intermediate dimension mismatch"
+    assert D == D2, "Output dimension mismatch"
 
     dtype = _check_tensors(x, w1, w2)
     o = torch.empty((H, B, D), dtype=x.dtype, device=x.device)
     L = _lib.lib()
-    with torch.cuda.device(x.device):
-        stream = torch.cuda.current_stream(x.device).cuda_stream
+    dev = _index(x)
+    with _OnDevice(dev):
+        stream = _stream_of(dev)
         if _tuned(D, E, dtype):
             x, w1, w2 = _dense(x), _dense(w1), _dense(w2)
             st = L.fmlp_fwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), o.data_ptr(), H, B, D, E, dtype,
@@ -144,15 +185,15 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     (need dx, need dw1 and dw2; FlashMLPFunction passes autograd's needs_input_grad) skips the
     programs of a gradient nobody asked for and returns None in its place.
     """
-    assert x.shape[0] == w1.shape[0], "Number of heads must match"
-    assert x.shape[0] == w2.shape[0], "Number of heads must match"
-    assert x.shape[2] == w1.shape[1], "Hidden dimension mismatch"
-    assert w1.shape[2] == w2.shape[1], "Intermediate dimension mismatch"
-    assert x.shape[2] == w2.shape[2], "Output dimension mismatch"
-    assert x.shape == do.shape, "Gradient shape mismatch"
-
     H, B, D = x.shape
-    E = w1.shape[2]
+    H1, D1, E = w1.shape
+    H2, E2, D2 = w2.shape
+    assert H == H1, "Number of heads must match"
+    assert H == H2, "Number of heads must match"
+    assert D == D1, "Hidden dimension mismatch"
+    assert E == E2, "Intermediate dimension mismatch"
+    assert D == D2, "Output dimension mismatch"
+    assert x.shape == do.shape, "Gradient shape mismatch"
 
     dtype = _check_tensors(x, w1, w2, do)
     need_dx, need_dw = bool(_needs[0]), bool(_needs[1])
@@ -164,11 +205,11 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     if not (need_dx or need_dw):
         return dx, dw1, dw2
     L = _lib.lib()
-    with torch.cuda.device(x.device):
-        stream = torch.cuda.current_stream(x.device).cuda_stream
+    dev = _index(x)
+    with _OnDevice(dev):
+        stream = _stream_of(dev)
         if _tuned(D, E, dtype):
             x, w1, w2, do = _dense(x), _dense(w1), _dense(w2), _dense(do)
-            dev = x.device.index if x.device.index is not None else torch.cuda.current_device()
             ws_bytes = _ws_bytes(dev, H, B, D, E, flags)
             try:
                 ws = _alloc_ws(ws_bytes, x.device)
