@@ -561,12 +561,32 @@ def run_mfma_ceiling(args):
             torch.cuda.synchronize()
             ms = _wall_ms(call_mix, max(args.steps, 50))
             mix[f"lds{lds_reads}_chains{chains}"] = round(mix_flops / (ms * 1e-3) / 1e12, 1)
+    # the dW role's mix: LDS bytes and SiLU-backward elements per MFMA, at one or two waves per
+    # SIMD (the grid holds that many workgroups of four waves per CU)
+    lib.fmlp_ceiling_act_mix.restype = ctypes.c_int
+    act_mix = {}
+    for lds8, el2, wps in ((0, 1, 2), (0, 1, 1), (2, 1, 2), (2, 1, 1), (3, 1, 2), (3, 1, 1),
+                           (0, 2, 2), (0, 2, 1), (2, 2, 2), (2, 2, 1)):
+        g = wps * ncu
+
+        def call_act():
+            r = lib.fmlp_ceiling_act_mix(ctypes.c_void_p(out.data_ptr()), mix_iters, lds8, el2, wps, g, st)
+            if r != 0:
+                raise RuntimeError(f"fmlp_ceiling_act_mix: hip error {r}")
+        for _ in range(args.warmup + 20):
+            call_act()
+        torch.cuda.synchronize()
+        ms = _wall_ms(call_act, max(args.steps, 50))
+        act_mix[f"lds{lds8 * 512}_elem{el2 / 2:g}_wps{wps}"] = round(g * 4 * mix_iters * 16 * 32768.0 / (ms * 1e-3) / 1e12, 1)
     peak = PEAK_TFLOPS["bf16"]
     line = {"metric": "sustained bf16 MFMA rate (v_mfma_f32_32x32x16_bf16, register operands)", "workload": "mfma_ceiling",
             "unit": "TFLOP/s", "peak": peak, "random": res["random"], "zero": res["zero"],
             "random_frac_of_peak": round(res["random"]["tflops"] / peak, 4),
             "with_per_mfma_work": {"unit": "TFLOP/s", "lds": "1 KB LDS read per wave per MFMA (A operand)",
                                    "chains": "sigmoid-like VALU chains (mul, exp, add, rcp) per MFMA", **mix},
+            "dw_role_mix": {"unit": "TFLOP/s", "lds": "LDS bytes per wave per MFMA",
+                            "elem": "SiLU-backward elements (h and dZ, packed to bf16) per lane per MFMA",
+                            "wps": "waves per SIMD", **act_mix},
             "config": {"grid": grid, "waves_per_simd": 2, "mfma_per_wave": iters * 4, "chains_per_wave": 4}}
     print(json.dumps(line), flush=True)
 

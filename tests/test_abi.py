@@ -189,4 +189,5 @@ def test_ceiling_library_exports_its_entry_point():
     out = subprocess.run(["nm", "-D", "--defined-only", str(lib)], capture_output=True, text=True, check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
     assert "fmlp_ceiling_mfma" in exported and "fmlp_ceiling_mix" in exported
+    assert "fmlp_ceiling_act_mix" in exported
     ctypes.CDLL(str(lib))  # loads without a GPU
