@@ -178,6 +178,18 @@ fmlp::GenArgs gen_args(const void* x, const void* w1, const void* w2, const void
   return g;
 }
 
+// 16-bit rows whose runs of 8 columns starting at multiples of 8 are aligned 16-byte vectors:
+// unit column stride, head and row strides multiples of 8 elements, 16-byte aligned base
+int vec_rows(const void* p, const long long* s, int io) {
+  if (io == FMLP_DTYPE_F32 || p == nullptr) return 0;
+  return (s[2] == 1 && s[1] % 8 == 0 && s[0] % 8 == 0 && aligned16(p)) ? 1 : 0;
+}
+// the same for runs of 4 columns starting at multiples of 4 (8-byte vectors)
+int vec_runs4(const void* p, const long long* s, int io) {
+  if (io == FMLP_DTYPE_F32 || p == nullptr) return 0;
+  return (s[2] == 1 && s[1] % 4 == 0 && s[0] % 4 == 0 && (reinterpret_cast<uintptr_t>(p) & 7u) == 0) ? 1 : 0;
+}
+
 }  // namespace
 
 FMLP_EXPORT int fmlp_abi_version(void) { return FMLP_ABI_VERSION; }
@@ -249,6 +261,8 @@ int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, 
         g.sw2[i] = sw2[i];
       }
     }
+    g.vec_x = vec_rows(x, g.sx, io);
+    if ((st = num_cus_current(&g.num_cus))) return st;
     e = fmlp::launch_gen_fwd(g, (hipStream_t)stream);
   }
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "forward launch: %s", hipGetErrorString(e));
@@ -272,10 +286,11 @@ FMLP_EXPORT int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, 
 
 FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   if (check_shape(H, B, D, E, dtype) != FMLP_OK) return 0;
-  if (!tuned_shape(D, E, io_of(dtype))) return 0;  // the generic kernels need no workspace
   if (dtype & FMLP_BWD_NO_DW) return 0;            // the dX programs alone use no workspace
   int cus = 0;
   if (num_cus_current(&cus) != FMLP_OK) return 0;
+  // the generic kernels: the fp32 partials of their dW programs' B split
+  if (!tuned_shape(D, E, io_of(dtype))) return fmlp::gen_plan(H, B, D, E, cus, (size_t)-1).ws_bytes;
   // the plan depends on the activation, which this query does not take: the largest over them
   size_t n = 0;
   for (int act = 0; act < 4; ++act) {
@@ -357,6 +372,31 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
         g.sw1[i] = sw1[i];
         g.sw2[i] = sw2[i];
         g.sdo[i] = sdo[i];
+      }
+    }
+    g.vec_x = vec_rows(x, g.sx, io);
+    g.vec_do = vec_rows(dout, g.sdo, io);
+    g.vec_w2 = vec_rows(w2, g.sw2, io);
+    g.vec_w1 = vec_runs4(w1, g.sw1, io);
+    if ((st = num_cus_current(&g.num_cus))) return st;
+    if (want_dw && B > 0) {
+      // B split of the dW programs within the workspace the caller gave (the static scratch for
+      // the no-allocation entry point; none: no split). A call that arrives here with the tuned
+      // path's workspace (a strided view of a tuned shape) uses what fits of it.
+      int cus = 0;
+      if ((st = num_cus_current(&cus))) return st;
+      const size_t room = noalloc ? fmlp::kScratchBytes
+                                  : (workspace != nullptr && aligned16(workspace) ? workspace_bytes : 0);
+      const fmlp::GenPlan gp = fmlp::gen_plan(H, B, D, E, cus, room);
+      if (gp.nS > 1) {
+        void* ws = workspace;
+        if (noalloc) {
+          e = fmlp::scratch_current_device(&ws);
+          if (e != hipSuccess) return fail(FMLP_ERR_HIP, "scratch lookup: %s", hipGetErrorString(e));
+        }
+        g.nS = gp.nS;
+        g.rows_per_split = gp.rows_per_split;
+        g.ws = ws;
       }
     }
     e = fmlp::launch_gen_bwd(g, (hipStream_t)stream);

@@ -88,7 +88,27 @@ struct GenArgs {
   int out_f32;  // outputs as fp32 (FMLP_OUT_F32)
   int hilo;     // dW products with hi/lo terms of h and dZ (FMLP_DW_HILO; 16-bit io)
   int want_dx = 1, want_dw = 1;  // FMLP_BWD_NO_DX / FMLP_BWD_NO_DW clear them
+  // rows of X / dO whose 8 consecutive 16-bit columns starting at any multiple of 8 are one
+  // aligned 16-byte vector (unit column stride, row and head strides multiples of 8 elements,
+  // 16-byte aligned base): set by the host, 16-bit io only
+  int vec_x = 0, vec_do = 0;
+  // the same for the rows of W2 (H, E, D) along d (16 bytes), and W1 (H, D, E) along e in
+  // 8-byte runs (unit column stride, strides multiples of 4 elements, 8-byte aligned base)
+  int vec_w2 = 0, vec_w1 = 0;
+  // backward B split of the dW programs (gen_plan): nS ranges of rows_per_split rows, fp32 partials
+  // in ws ([nS][H][E][D] for dW2, then [nS][H][D][E] for dW1) when nS > 1
+  int nS = 1, rows_per_split = 0;
+  void* ws = nullptr;
+  int num_cus = 256;  // compute units of the current device (the forward / dX E split)
 };
+struct GenPlan {
+  int nS;
+  int rows_per_split;
+  size_t ws_bytes;
+};
+// B split of the generic dW programs for a device with num_cus CUs, within max_ws bytes of
+// workspace (a split that does not fit is not taken: nS = 1 needs none)
+GenPlan gen_plan(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t max_ws);
 hipError_t launch_gen_fwd(const GenArgs& a, hipStream_t st);
 hipError_t launch_gen_bwd(const GenArgs& a, hipStream_t st);
 bool gen_supports_d(int64_t D);

@@ -225,10 +225,17 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
                             _ptr(dw1), _ptr(dw2), H, B, D, E, flags, _act_code(activation),
                             ws.data_ptr() if ws is not None else None, ws_bytes, stream)
         else:
+            # the generic kernels' dW programs split B with fp32 partials in the workspace when
+            # it is given; without one (it does not fit) they run unsplit
+            ws_bytes = _ws_bytes(dev, H, B, D, E, flags)
+            try:
+                ws = _alloc_ws(ws_bytes, x.device)
+            except torch.OutOfMemoryError:
+                ws, ws_bytes = None, 0
             st = L.fmlp_bwd_strided(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), do.data_ptr(), _ptr(dx),
                                     _ptr(dw1), _ptr(dw2), H, B, D, E, _lib.strides(x), _lib.strides(w1),
-                                    _lib.strides(w2), _lib.strides(do), flags, _act_code(activation), None, 0,
-                                    stream)
+                                    _lib.strides(w2), _lib.strides(do), flags, _act_code(activation),
+                                    ws.data_ptr() if ws is not None else None, ws_bytes, stream)
     _lib.check(st, "backward")
     return dx, dw1, dw2
 

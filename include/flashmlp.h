@@ -134,7 +134,10 @@ int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int
 /* Bytes of device workspace fmlp_bwd / fmlp_bwd_strided need for these shapes and dtype flags
  * on the current device, whatever the activation (0 when none is needed). Every backward flag
  * can change it (FMLP_DW_HILO, FMLP_BWD_RECOMPUTE, FMLP_BWD_STORE_DZ and FMLP_BWD_NO_DX change
- * the plan; with FMLP_BWD_NO_DW it is 0): query it with the flags of the call it is for. */
+ * the plan; with FMLP_BWD_NO_DW it is 0): query it with the flags of the call it is for. For
+ * shapes the tuned kernels do not take, it is the fp32 partials of the generic dW programs'
+ * B split; those calls (and fmlp_bwd_strided calls whose views send a tuned shape to the
+ * generic kernels) accept any workspace, NULL included, and split B only as far as it fits. */
 size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
 /* 1 when fmlp_bwd takes the stored-dZ form for these shapes, dtype flags and activation on the

@@ -182,3 +182,54 @@ def test_module_fp32_and_small_d():
     reference.torch_fwd(xc, w1, w2, "silu").sum().backward()
     for got, ref in ((x.grad, xc.grad), (m.w1.grad, w1.grad), (m.w2.grad, w2.grad)):
         assert _normrel(got.cpu(), ref) <= 1e-4
+
+
+def _bwd_strided(x, w1, w2, do, act, ws_bytes):
+    """fmlp_bwd_strided on dense tensors with a workspace of ws_bytes (0: none)."""
+    L = _lib.lib()
+    H, B, D = x.shape
+    E = w1.shape[2]
+    code = {torch.float16: _lib.FMLP_DTYPE_F16, torch.bfloat16: _lib.FMLP_DTYPE_BF16,
+            torch.float32: _lib.FMLP_DTYPE_F32}[x.dtype]
+    outs = (torch.empty_like(x), torch.empty_like(w1), torch.empty_like(w2))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=x.device) if ws_bytes else None
+    p = lambda t: ctypes.c_void_p(t.data_ptr()) if t is not None else None
+    st = L.fmlp_bwd_strided(p(x), p(w1), p(w2), p(do), *(p(t) for t in outs), H, B, D, E, _lib.strides(x),
+                            _lib.strides(w1), _lib.strides(w2), _lib.strides(do), code, _lib.ACT_CODES[act],
+                            p(ws), ws_bytes, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    _lib.check(st, "backward (strided)")
+    torch.cuda.synchronize()
+    return outs
+
+
+@pytest.mark.parametrize("D,dt,act", [(32, torch.bfloat16, "silu"), (256, torch.float16, "sigmoid"),
+                                      (64, torch.float32, "leaky_relu")], ids=["D32-bf16", "D256-fp16", "D64-fp32"])
+def test_generic_dw_b_split(D, dt, act):
+    """The generic dW programs split B over workgroups when the workspace allows (fp32 partials,
+    then a reduction in split order): with the queried workspace the results match the oracle at
+    the usual bars, and the unsplit run (no workspace) within the summation-order difference."""
+    H, B, E = 2, 3000, 136
+    x, w1, w2, do = make_inputs(H, B, D, E, dt, seed=81)
+    L = _lib.lib()
+    code = {torch.float16: _lib.FMLP_DTYPE_F16, torch.bfloat16: _lib.FMLP_DTYPE_BF16,
+            torch.float32: _lib.FMLP_DTYPE_F32}[dt]
+    assert L.fmlp_shape_tuned(D, E, code) == 0
+    n = L.fmlp_bwd_workspace_bytes(H, B, D, E, code)
+    _say(f"[generic] B split H={H} B={B} D={D} E={E} {dt} act='{act}' workspace={n}")
+    assert n > 0, "this shape should split B"
+    xd, w1d, w2d, dod = (t.cuda() for t in (x, w1, w2, do))
+    split = [t.cpu() for t in _bwd_strided(xd, w1d, w2d, dod, act, n)]
+    whole = [t.cpu() for t in _bwd_strided(xd, w1d, w2d, dod, act, 0)]
+    _, rdx, rdw1, rdw2 = reference.autograd_grads(x, w1, w2, do, act)
+    assert torch.equal(split[0], whole[0])  # dX does not depend on the split
+    if dt == torch.float32:
+        for got, ref in zip(split, (rdx, rdw1, rdw2)):
+            assert _normrel(got, ref) <= 1e-4
+    else:
+        _, edw1, edw2 = emulate.emu_bwd(x, w1, w2, do, act, dt)
+        assert _fail_frac(split[0], rdx) == 0.0
+        for got, emu, ref in ((split[1], edw1, rdw1), (split[2], edw2, rdw2)):
+            assert _fail_frac(got, emu) == 0.0
+            assert _normrel(got, ref) <= 1e-2
+    for a, b in zip(split[1:], whole[1:]):
+        assert _normrel(a, b) <= (1e-5 if dt == torch.float32 else 5e-3)  # summation order
