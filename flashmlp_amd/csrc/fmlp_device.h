@@ -263,6 +263,21 @@ __device__ __forceinline__ void buf_load16_lds(const i32x4& rsrc, unsigned byte_
                : "v"(byte_off), "s"(rsrc), "s"(m0)
                : "memory", "m0");
 }
+// The same with the non-temporal cache policy, for data a kernel reads exactly once and nothing
+// reads after it (the stored dZ): its lines are not kept in the caches, so they do not evict
+// what other streams still use.
+__device__ __forceinline__ void buf_load16_lds_nt(const i32x4& rsrc, unsigned byte_off, int lds_byte_off) {
+  const unsigned m0 = (unsigned)__builtin_amdgcn_readfirstlane(
+      (int)(unsigned)(uintptr_t)((FMLP_LDS char*)fmlp_lds + lds_byte_off));
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen nt lds"
+               :
+               : "v"(byte_off), "s"(rsrc), "s"(m0)
+               : "memory", "m0");
+}
+// cache-policy operand of the buffer store builtins: non-temporal (data written once, read once
+// by a later kernel)
+constexpr int CPOL_NT = 2;
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt");
