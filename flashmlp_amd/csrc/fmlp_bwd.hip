@@ -125,38 +125,52 @@ constexpr int DX_NSLOT = 8;  // chunk ring slots (128 D bytes each)
 constexpr int DX_PF = 4;     // chunks requested ahead of the one read
 static_assert(DX_PF <= DX_NSLOT - 2, "a slot is reloaded only after the barrier that retires its last reader");
 
-template <bool BF16, int D, int ACT>
+// DES = 2 (E split, D = 64 only: grids of 256-row dX programs that leave CUs idle): a program
+// owns 128 rows; waves 0-3 walk the first half of the E-chunks and waves 4-7 the second, each
+// half through an LDS ring of its own, and the second half's partial dX tile is added to the
+// first's through LDS at the end.
+template <int D, int DES>
+__host__ __device__ constexpr int dx2_rows() { return DX2_ROWS / DES; }
+
+template <bool BF16, int D, int ACT, int DES = 1>
 __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* __restrict__ W1,
                                          const u16* __restrict__ W2, const u16* __restrict__ dO,
                                          void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32,
                                          int t) {
+  static_assert(DES == 1 || (DES == 2 && D == 64), "E split");
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr unsigned SLOT = 128u * D;
   constexpr unsigned W2OFF = 64u * D;
-  constexpr int NDMA = D / 64;  // 16-byte pieces per lane per chunk
+  constexpr int NTP = DX2_NT / DES;      // threads of one E part
+  constexpr int NDMA = 8 * D / NTP;      // 16-byte pieces per lane per chunk
   constexpr int N1 = 2 * KS, N2 = 2 * NTN;
   constexpr int PD = 3;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
-  
+  const int part = DES == 1 ? 0 : wave >> 2;       // E part
+  const int wp = DES == 1 ? wave : (wave & 3);     // wave within the part
+
   const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
   const int NC = (E + 31) >> 5;
-  const bool late = wave >= 4;  // VALU-first half of the workgroup
+  const int NCP = (NC + DES - 1) / DES;             // chunks per part: global chunk c0 + ci
+  const int c0 = part * NCP;
+  const int RB = part * DX_NSLOT * (int)SLOT;       // this part's ring
+  const bool late = wave >= 4;  // VALU-first half of the workgroup (the second part when split)
 
   const u16* Xh = X + (size_t)h * B * D;
   const u16* dOh = dO + (size_t)h * B * D;
   const u16* W1h = W1 + (size_t)h * D * E;
   const u16* W2h = W2 + (size_t)h * E * D;
-  const int b_wave = bt * DX2_ROWS + wave * 32;
+  const int b_wave = bt * dx2_rows<D, DES>() + wp * 32;
 
   // ---- staging pieces: piece p (16 bytes at slot offset 16 p) of a chunk ----
   unsigned dmaOff[NDMA];
   int dmaCol[NDMA];  // W1c pieces: first chunk column (masked against E); W2c pieces: -1
 #pragma unroll
   for (int k = 0; k < NDMA; ++k) {
-    const unsigned p = k * DX2_NT + wave * 64 + lane;
+    const unsigned p = k * NTP + wp * 64 + lane;
     if (p < 4u * D) {  // W1c row r, logical chunk q
       const unsigned r = p >> 2, q = (p & 3u) ^ ((r >> 2) & 3u);
       dmaOff[k] = r * (unsigned)E * 2u + q * 16u;
@@ -168,21 +182,24 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
       dmaCol[k] = -1;
     }
   }
-  // chunk staging: buffer-to-LDS loads DX_PF chunks ahead into a DX_NSLOT-slot ring
-  auto dma_chunk = [&](int c) {
-    const int lim = E - c * 32;
-    const int rem = D * E * 2 - 64 * c;
+  // chunk staging: buffer-to-LDS loads DX_PF chunks ahead into a DX_NSLOT-slot ring; part chunk
+  // ci is global chunk c0 + ci, and chunks past the part's share (or past E) load as zeros
+  auto dma_chunk = [&](int ci) {
+    const int c = c0 + ci;
+    const bool mine = ci < NCP;
+    const int lim = mine ? E - c * 32 : 0;
+    const int rem = mine ? D * E * 2 - 64 * c : 0;
     const i32x4 r1 = make_rsrc_words(W1h + (size_t)c * 32, rem > 0 ? rem : 0);
     const i32x4 r2 = make_rsrc_words(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
-    const int slot = (c & (DX_NSLOT - 1)) * (int)SLOT + wave * 1024;
+    const int slot = RB + (ci & (DX_NSLOT - 1)) * (int)SLOT + wp * 1024;
 #pragma unroll
     for (int k = 0; k < NDMA; ++k) {
       // W1c or W2c piece (wave-uniform): word-wise selects keep the loop body one basic block
-      const bool w1 = (unsigned)(k * DX2_NT + wave * 64) < 4u * D;
+      const bool w1 = (unsigned)(k * NTP + wp * 64) < 4u * D;
       i32x4 rr;
 #pragma unroll
       for (int i = 0; i < 4; ++i) rr[i] = __builtin_amdgcn_readfirstlane(w1 ? r1[i] : r2[i]);
-      buf_load16_lds(rr, dmaCol[k] < lim ? dmaOff[k] : BUF_OOB, slot + k * DX2_NT * 16);
+      buf_load16_lds(rr, dmaCol[k] < lim ? dmaOff[k] : BUF_OOB, slot + k * NTP * 16);
     }
   };
 
@@ -232,7 +249,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
   auto mfma_phase = [&](auto G2, int c) {
     constexpr bool DO_G2 = decltype(G2)::value;
     constexpr int M2 = DO_G2 ? N2 : 0, NOPS = N1 + M2;
-    const int base1 = (c & (DX_NSLOT - 1)) * (int)SLOT, base2 = ((c - 1) & (DX_NSLOT - 1)) * (int)SLOT;
+    const int base1 = RB + (c & (DX_NSLOT - 1)) * (int)SLOT, base2 = RB + ((c - 1) & (DX_NSLOT - 1)) * (int)SLOT;
     auto fetch = [&](int j) -> u32x4 {
       const int q = sched_index(j, N1, M2);
       if (sched_is_g2(j, N1, M2)) {
@@ -265,7 +282,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
     }
   };
   auto g2_only = [&](int c) {  // dX += dZ(c) W1c(c)^T
-    const int base2 = (c & (DX_NSLOT - 1)) * (int)SLOT;
+    const int base2 = RB + (c & (DX_NSLOT - 1)) * (int)SLOT;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
@@ -297,12 +314,14 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
   chunk_end();
   const std::true_type T{};
   const std::false_type F{};
+  // (chunk indices below are part-relative; both parts run NCP iterations, so the workgroup
+  // barriers line up)
   if (!late) {
     chunk_begin(0);
     mfma_phase(F, 0);
     valu_phase();
     chunk_end();
-    for (int c = 1; c < NC; ++c) {
+    for (int c = 1; c < NCP; ++c) {
       mfma_phase(T, c);
       chunk_begin(c);  // staged between the phases: fewer LDS writes next to the operand reads
       valu_phase();
@@ -312,7 +331,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
     chunk_begin(0);
     mfma_phase(F, 0);
     chunk_end();
-    for (int c = 1; c < NC; ++c) {
+    for (int c = 1; c < NCP; ++c) {
       chunk_begin(c);
       valu_phase();
       mfma_phase(T, c);
@@ -320,8 +339,32 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
     }
     valu_phase();
   }
-  g2_only(NC - 1);
+  g2_only(NCP - 1);
   wait_vmcnt<0>();  // chunk loads past the last are still landing (as zeros)
+  if constexpr (DES == 2) {  // part 1 hands its partial dX tile to part 0 through LDS (the rings)
+    asm volatile("" ::: "memory");
+    __syncthreads();
+    const int ob = wp * (NTN * 4096);  // per wave NTN x 4 x [64 lanes][16 bytes]
+    if (part == 1) {
+#pragma unroll
+      for (int nt = 0; nt < NTN; ++nt)
+#pragma unroll
+        for (int i4 = 0; i4 < 4; ++i4)
+          lds_write16(ob + ((nt * 4 + i4) * 64 + lane) * 16,
+                      u32x4{__float_as_uint(acc[nt][4 * i4]), __float_as_uint(acc[nt][4 * i4 + 1]),
+                            __float_as_uint(acc[nt][4 * i4 + 2]), __float_as_uint(acc[nt][4 * i4 + 3])});
+    }
+    __syncthreads();
+    if (part == 1) return;
+#pragma unroll
+    for (int nt = 0; nt < NTN; ++nt)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const u32x4 v = lds_read16(ob + ((nt * 4 + i4) * 64 + lane) * 16);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[nt][4 * i4 + j] += __uint_as_float(v[j]);
+      }
+  }
   store_rows<BF16, D>(acc, dX, (size_t)h * B * D, B, b_wave, g, l32, outf32);
 }
 
@@ -645,12 +688,12 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
   }
 }
 
-// dX programs as their own launch (FMLP_BWD_UNIFIED=0): 8 waves, two per SIMD.
-template <bool BF16, int D, int ACT>
+// dX programs as their own launch (FMLP_BWD_UNIFIED=0, FMLP_BWD_NO_DW): 8 waves, two per SIMD.
+template <bool BF16, int D, int ACT, int DES>
 __global__ void __launch_bounds__(DX2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
-  dx2_body<BF16, D, ACT>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32, xcd_remap(blockIdx.x, gridDim.x));
+  dx2_body<BF16, D, ACT, DES>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32, xcd_remap(blockIdx.x, gridDim.x));
 }
 
 template <bool BF16, int D, int ACT, bool HILO, bool DZ>
@@ -668,7 +711,7 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 // use 8 waves (two per SIMD); the dynamic LDS is the dW role's (the larger). Each role's
 // tiles are remapped onto XCDs within its own range (exact when its count is a multiple of 8).
 static_assert(DW2_NT == DX2_NT, "both roles run with the same workgroup size");
-template <bool BF16, int D, int ACT, bool HILO>
+template <bool BF16, int D, int ACT, bool HILO, int DES>
 __global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dX, void* __restrict__ dW1, void* __restrict__ dW2,
@@ -680,7 +723,7 @@ bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     dw2_body<BF16, D, ACT, HILO>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32, xcd_remap(bw, n_dw));
   } else {
     const int bx = dx_first ? b : b - n_dw;
-    dx2_body<BF16, D, ACT>(X, W1, W2, dO, dX, B, E, dx_tiles_per_head, outf32, xcd_remap(bx, n_dx));
+    dx2_body<BF16, D, ACT, DES>(X, W1, W2, dO, dX, B, E, dx_tiles_per_head, outf32, xcd_remap(bx, n_dx));
   }
 }
 
@@ -986,14 +1029,21 @@ long long rows_for_split(long long B, long long ns) {
 }
 
 BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int dz_mode, int num_cus,
-                  size_t max_ws) {
+                  size_t max_ws, int fixed_des = 0) {
+  // the dX programs' E split follows the default dW mode's plan, so dX does not depend on the
+  // dW mode (FMLP_DW_HILO changes only dW)
+  if (hilo && D == 64 && fixed_des == 0)
+    fixed_des = make_plan(H, B, D, E, act, false, DZ_NEVER, num_cus, max_ws).dx_es;
   BwdPlan p{};
   p.nE = (int)((E + DW_ET - 1) / DW_ET);
   const long long base = H * (long long)p.nE, N = num_cus > 0 ? num_cus : 1;
-  p.dx_tiles_per_head = (int)((B + DX2_ROWS - 1) / DX2_ROWS);
-  p.n_dx = (long long)p.dx_tiles_per_head * H;
   auto ws_for = [&](long long ns) { return ns > 1 ? (size_t)2 * ns * H * E * D * sizeof(float) : (size_t)0; };
-  const double tx = kPlanFixedUs + 256.0 * E * (3.0 * D + valu_dx(act) * kPlanValuMacs) / kPlanRate;
+  // dX programs of 256 rows, or at D = 64 of 128 rows with E in two parts (half the time each)
+  auto n_dx_for = [&](int des) { return H * ((B + DX2_ROWS / des - 1) / (DX2_ROWS / des)); };
+  auto tx_for = [&](int des) {
+    return kPlanFixedUs + (double)(DX2_ROWS / des) * E * (3.0 * D + valu_dx(act) * kPlanValuMacs) / kPlanRate;
+  };
+  const int max_des = D == 64 ? 2 : 1;
   const double w_per_row = 128.0 * ((hilo ? 6.0 : 4.0) * D + valu_dw(act) * kPlanValuMacs) / kPlanRate;
   // candidates nS = 1, 2, 4, ... up to B / 256 and two dW programs per CU (which keeps the fp32
   // partials within 64 MiB at D <= 128 on 256 CUs), whose workspace fits max_ws
@@ -1005,26 +1055,39 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
   // (1: dW programs first, 2: dX programs first)
   static const int ns_env = env_int("FMLP_BWD_NS", 0);
   static const int order_env = env_int("FMLP_BWD_ORDER", 0);
+  // FMLP_BWD_DXES (read once per process) forces the dX programs' E split (1 or 2, D = 64)
+  static const int des_env = env_int("FMLP_BWD_DXES", 0);
   double best_t = 0.0;
   long long best_ns = 1;
   bool best_dx_first = false;
-  for (long long ns = 1; ns <= (ns_env > 0 ? 1 : cap); ns *= 2) {
-    const long long want = ns_env > 0 ? (ns_env < max_ns ? ns_env : max_ns) : ns;
-    const long long rps = rows_for_split(B, want), eff = B > rps ? (B + rps - 1) / rps : 1;
-    if (eff > 1 && ws_for(eff) > max_ws) break;
-    const double tw = kPlanFixedUs + (double)rps * w_per_row;
-    const long long n_dw = base * eff;
-    const double red = eff > 1 ? kPlanLaunchUs + (double)(2 * eff + 1) * H * E * D * 4.0 / kPlanHbmBytesPerUs : 0.0;
-    for (int o = 1; o <= 2; ++o) {
-      if (order_env && o != order_env) continue;
-      const double t = (o == 1 ? list_makespan(n_dw, tw, p.n_dx, tx, N) : list_makespan(p.n_dx, tx, n_dw, tw, N)) + red;
-      if (best_t == 0.0 || t < best_t) {
-        best_t = t;
-        best_ns = eff;
-        best_dx_first = o == 2;
+  int best_des = 1;
+  for (int des = 1; des <= max_des; ++des) {
+    if (des_env > 0 && des != des_env) continue;
+    if (fixed_des > 0 && des != fixed_des) continue;
+    const long long n_dx = n_dx_for(des);
+    const double tx = tx_for(des);
+    for (long long ns = 1; ns <= (ns_env > 0 ? 1 : cap); ns *= 2) {
+      const long long want = ns_env > 0 ? (ns_env < max_ns ? ns_env : max_ns) : ns;
+      const long long rps = rows_for_split(B, want), eff = B > rps ? (B + rps - 1) / rps : 1;
+      if (eff > 1 && ws_for(eff) > max_ws) break;
+      const double tw = kPlanFixedUs + (double)rps * w_per_row;
+      const long long n_dw = base * eff;
+      const double red = eff > 1 ? kPlanLaunchUs + (double)(2 * eff + 1) * H * E * D * 4.0 / kPlanHbmBytesPerUs : 0.0;
+      for (int o = 1; o <= 2; ++o) {
+        if (order_env && o != order_env) continue;
+        const double t = (o == 1 ? list_makespan(n_dw, tw, n_dx, tx, N) : list_makespan(n_dx, tx, n_dw, tw, N)) + red;
+        if (best_t == 0.0 || t < best_t) {
+          best_t = t;
+          best_ns = eff;
+          best_dx_first = o == 2;
+          best_des = des;
+        }
       }
     }
   }
+  p.dx_es = best_des;
+  p.dx_tiles_per_head = (int)((B + DX2_ROWS / best_des - 1) / (DX2_ROWS / best_des));
+  p.n_dx = (long long)p.dx_tiles_per_head * H;
   // Stored-dZ form: the dW launch alone (programs dealt over the CUs) and its reduction, then
   // storing dZ and streaming it back through the dX GEMM (memory-bound: a rate per byte, in the
   // same time units, and a fixed part for the extra launch). Fitted to the same-box times of
@@ -1056,6 +1119,8 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
   if (p.dz) {
     best_ns = best_dz_ns;
     best_dx_first = false;
+    p.dx_es = 1;
+    p.dx_tiles_per_head = (int)((B + DX2_ROWS - 1) / DX2_ROWS);
   }
   const long long rps = rows_for_split(B, best_ns);
   p.nS = (int)(B > rps ? (B + rps - 1) / rps : 1);
@@ -1106,11 +1171,13 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo,
   return p;
 }
 
-template <bool BF16, int D, int ACT>
+template <bool BF16, int D, int ACT, int DES>
 static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
   if (p.n_dw > 0x7fffffffLL || p.n_dx > 0x7fffffffLL || p.n_dw + p.n_dx > 0x7fffffffLL) return hipErrorInvalidValue;
   hipError_t e;
-  const size_t lds = 1280u * D;  // the dW role's: two weight tiles and three subtile pairs (256 D bytes each)
+  // the dW role's: two weight tiles and three subtile pairs (256 D bytes each); at least the
+  // dX role's rings (one or two parts of DX_NSLOT slots of 128 D bytes)
+  constexpr size_t lds = std::max<size_t>(1280u * D, (size_t)DES * DX_NSLOT * 128u * D);
   auto reduce = [&]() {          // sum of the dW programs' fp32 partials when B is split
     if (p.nS <= 1) return hipSuccess;
     const size_t items = 2 * ((size_t)a.H * a.E * a.D / 4);
@@ -1158,7 +1225,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
                          p.dx_tiles_per_head, p.dx_first ? 1 : 0, a.out_f32 ? 1 : 0);
       return hipGetLastError();
     };
-    e = a.dw_hilo ? launch_u(bwd_kernel<BF16, D, ACT, true>) : launch_u(bwd_kernel<BF16, D, ACT, false>);
+    e = a.dw_hilo ? launch_u(bwd_kernel<BF16, D, ACT, true, DES>) : launch_u(bwd_kernel<BF16, D, ACT, false, DES>);
     if (e != hipSuccess) return e;
     return reduce();
   }
@@ -1177,8 +1244,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     if ((e = reduce()) != hipSuccess) return e;
   }
   if (p.n_dx > 0 && a.want_dx) {
-    const size_t lds_x = (size_t)DX_NSLOT * 128u * D;  // the chunk ring
-    auto k = dx2_kernel<BF16, D, ACT>;
+    const size_t lds_x = (size_t)DES * DX_NSLOT * 128u * D;  // the chunk ring(s)
+    auto k = dx2_kernel<BF16, D, ACT, DES>;
     static std::atomic<unsigned long long> lds_set{0};
     e = set_lds_once((const void*)k, (int)lds_x, lds_set);
     if (e != hipSuccess) return e;
@@ -1190,13 +1257,21 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   return hipSuccess;
 }
 
+template <bool BF16, int D, int ACT>
+static hipError_t launch_bwd_e(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
+  if constexpr (D == 64) {
+    if (p.dx_es == 2) return launch_bwd_t<BF16, D, ACT, 2>(a, p, st);
+  }
+  return launch_bwd_t<BF16, D, ACT, 1>(a, p, st);
+}
+
 template <bool BF16, int D>
 static hipError_t launch_bwd_a(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
   switch (a.act) {
-    case ACT_SILU: return launch_bwd_t<BF16, D, ACT_SILU>(a, p, st);
-    case ACT_LEAKY: return launch_bwd_t<BF16, D, ACT_LEAKY>(a, p, st);
-    case ACT_SIGMOID: return launch_bwd_t<BF16, D, ACT_SIGMOID>(a, p, st);
-    default: return launch_bwd_t<BF16, D, ACT_NONE>(a, p, st);
+    case ACT_SILU: return launch_bwd_e<BF16, D, ACT_SILU>(a, p, st);
+    case ACT_LEAKY: return launch_bwd_e<BF16, D, ACT_LEAKY>(a, p, st);
+    case ACT_SIGMOID: return launch_bwd_e<BF16, D, ACT_SIGMOID>(a, p, st);
+    default: return launch_bwd_e<BF16, D, ACT_NONE>(a, p, st);
   }
 }
 

@@ -40,6 +40,7 @@ struct BwdPlan {
   int nS;              // B splits for the dW programs
   int rows_per_split;  // multiple of 32
   int dx_tiles_per_head;
+  int dx_es;           // dX programs: 1 = 256 rows, all E-chunks; 2 = 128 rows, E in two parts (D = 64)
   bool dx_first;       // single-launch order: dX programs before the dW programs
   long long n_dw, n_dx;
   bool dz;             // stored-dZ form

@@ -155,10 +155,15 @@ def test_bwd_falls_back_to_recompute_when_workspace_does_not_fit(monkeypatch):
     from flashmlp_amd import _lib
 
     fmm = importlib.import_module("flashmlp_amd.flashmlp")
-    H, B, D, E, dt, act = 8, 4097, 64, 2048, torch.float16, "sigmoid"
+    # the first of these shapes for which the plan takes the stored-dZ form (the choice is the
+    # plan's estimate, so the shape is looked up rather than assumed)
+    dt, act = torch.float16, "sigmoid"
     code, act_code = _lib.FMLP_DTYPE_F16, _lib.ACT_CODES[act]
-    assert _lib.lib().fmlp_bwd_stores_dz(H, B, D, E, code, act_code) == 1, "this shape should take the stored-dZ form"
-    assert _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, code | _lib.FMLP_BWD_RECOMPUTE) < (64 << 20)
+    shapes = [(8, 4097, 64, 2048), (8, 8192, 128, 1024), (16, 8192, 128, 1024), (32, 8192, 128, 1024)]
+    found = [s for s in shapes if _lib.lib().fmlp_bwd_stores_dz(*s, code, act_code) == 1
+             and _lib.lib().fmlp_bwd_workspace_bytes(*s, code | _lib.FMLP_BWD_RECOMPUTE) < (64 << 20)]
+    assert found, "no candidate shape takes the stored-dZ form with a recompute workspace under 64 MiB"
+    H, B, D, E = found[0]
     _say(f"[api] workspace fallback H={H} B={B} D={D} E={E} {dt} act='{act}'")
     x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=61))
     ref = fm.flashmlp_bwd(x, w1, w2, do, act, recompute=True)
