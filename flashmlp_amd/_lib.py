@@ -42,6 +42,9 @@ SIGNATURES = {
     "fmlp_fwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp]),
     "fmlp_fwd_strided": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p, _i64p,
                                         ctypes.c_int, ctypes.c_int, _vp]),
+    "fmlp_fwd_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, ctypes.c_int]),
+    "fmlp_fwd_ws": (ctypes.c_int, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _vp,
+                                   ctypes.c_size_t, _vp]),
     "fmlp_bwd_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, ctypes.c_int]),
     "fmlp_bwd_stores_dz": (ctypes.c_int, [_i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int]),
     "fmlp_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int,

@@ -227,7 +227,8 @@ FMLP_EXPORT int fmlp_shape_tuned(int64_t D, int64_t E, int dtype) { return tuned
 namespace {
 
 int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D, int64_t E,
-             const int64_t* sx, const int64_t* sw1, const int64_t* sw2, int dtype, int act, void* stream) {
+             const int64_t* sx, const int64_t* sw1, const int64_t* sw2, int dtype, int act, void* ws, size_t ws_bytes,
+             void* stream) {
   if (dtype & FMLP_DW_HILO) return fail(FMLP_ERR_INVALID_ARG, "FMLP_DW_HILO applies to the backward only");
   if (dtype & (FMLP_BWD_RECOMPUTE | FMLP_BWD_STORE_DZ | FMLP_BWD_NO_DX | FMLP_BWD_NO_DW))
     return fail(FMLP_ERR_INVALID_ARG,
@@ -242,7 +243,7 @@ int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, 
   const int io = io_of(dtype);
   const size_t es = elem_bytes(io);
   if ((st = check_ptr(x, "x", rows, es)) || (st = check_ptr(w1, "w1", wts, es)) || (st = check_ptr(w2, "w2", wts, es)) ||
-      (st = check_ptr(o, "o", rows, (dtype & FMLP_OUT_F32) ? 4 : es)))
+      (st = check_ptr(o, "o", rows, (dtype & FMLP_OUT_F32) ? 4 : es)) || (st = check_ptr(ws, "ws", ws != nullptr)))
     return st;
   if (!rows) return ok();
   const bool dense = sx == nullptr || (is_dense3(sx, B, D) && is_dense3(sw1, D, E) && is_dense3(sw2, E, D));
@@ -251,6 +252,8 @@ int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, 
     int cus = 0;
     if ((st = num_cus_current(&cus))) return st;
     fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, io == FMLP_DTYPE_BF16, act, (dtype & FMLP_OUT_F32) != 0, cus};
+    a.ws = ws;
+    a.ws_bytes = ws != nullptr ? ws_bytes : 0;
     e = fmlp::launch_fwd(a, (hipStream_t)stream);
   } else {
     fmlp::GenArgs g = gen_args(x, w1, w2, nullptr, o, nullptr, nullptr, nullptr, H, B, D, E, dtype, act);
@@ -273,7 +276,20 @@ int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, 
 
 FMLP_EXPORT int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
                          int64_t E, int dtype, int act, void* stream) {
-  return fwd_impl(x, w1, w2, o, H, B, D, E, nullptr, nullptr, nullptr, dtype, act, stream);
+  return fwd_impl(x, w1, w2, o, H, B, D, E, nullptr, nullptr, nullptr, dtype, act, nullptr, 0, stream);
+}
+
+FMLP_EXPORT size_t fmlp_fwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
+  if (check_shape(H, B, D, E, dtype) != FMLP_OK || !tuned_shape(D, E, io_of(dtype))) return 0;
+  int cus = 0;
+  if (num_cus_current(&cus) != FMLP_OK) return 0;
+  return fmlp::fwd_plan(H, B, D, E, cus, (size_t)-1).ws_bytes;
+}
+
+FMLP_EXPORT int fmlp_fwd_ws(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
+                            int64_t E, int dtype, int act, void* workspace, size_t workspace_bytes, void* stream) {
+  return fwd_impl(x, w1, w2, o, H, B, D, E, nullptr, nullptr, nullptr, dtype, act, workspace, workspace_bytes,
+                  stream);
 }
 
 FMLP_EXPORT int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B,
@@ -281,7 +297,7 @@ FMLP_EXPORT int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, 
                                  const int64_t* w2_strides, int dtype, int act, void* stream) {
   if (x_strides == nullptr || w1_strides == nullptr || w2_strides == nullptr)
     return fail(FMLP_ERR_INVALID_ARG, "stride arrays must not be NULL");
-  return fwd_impl(x, w1, w2, o, H, B, D, E, x_strides, w1_strides, w2_strides, dtype, act, stream);
+  return fwd_impl(x, w1, w2, o, H, B, D, E, x_strides, w1_strides, w2_strides, dtype, act, nullptr, 0, stream);
 }
 
 FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {

@@ -20,6 +20,7 @@
 //     no LDS store instructions); one workgroup barrier per two chunks.
 #include "fmlp_device.h"
 #include "fmlp_launch.h"
+#include <algorithm>
 #include <type_traits>
 
 namespace fmlp {
@@ -34,6 +35,28 @@ namespace fmlp {
 // sets of waves on the same rows, each walking half of the E-chunks through a ring of its own
 // (one workgroup per CU, two waves per SIMD instead of one); the two partial O tiles are added
 // through LDS at the end.
+// Split tiles (fwd_plan): the last n_split tiles in row-block-major order (tile (h, bt) at
+// bt H + h; the ragged last tiles of the heads first) are split; the first n_main workgroups
+// each own one of the other tiles, enumerated head by head (split_tile / main_tile); every later
+// workgroup owns one of xs E-ranges of nct chunks of split tile (b - n_main) / xs and stores its
+// fp32 partial O tile to ws (one [BB][D] block per workgroup), which fwd_reduce_kernel sums in
+// part order and rounds.
+struct TileId {
+  int h, bt;
+};
+// split tile s of n_split (H heads, T tiles per head)
+__device__ __forceinline__ TileId split_tile(int s, int n_split, int H, int T) {
+  const int t = H * T - n_split + s;
+  return TileId{t % H, t / H};
+}
+// whole tile m: rem = n_split = a H + b leaves heads h < H - b with T - a tiles, the others T - a - 1
+__device__ __forceinline__ TileId main_tile(int m, int n_split, int H, int T) {
+  const int a = n_split / H, b = n_split - a * H;
+  const int first = (H - b) * (T - a);
+  if (m < first) return TileId{m / (T - a), m % (T - a)};
+  const int m2 = m - first, tb = T - a - 1;
+  return TileId{H - b + m2 / tb, m2 % tb};
+}
 __host__ __device__ constexpr int fwd_waves(int D) { return D / 16; }
 constexpr int FWD_NSLOT = 8;  // LDS ring slots (chunks)
 constexpr int FWD_PF = 4;     // chunks loaded ahead (with one barrier per chunk)
@@ -42,7 +65,8 @@ constexpr int FWD_SB = 2;     // chunk iterations per workgroup barrier
 template <bool BF16, int D, int ACT, int ES>
 __global__ void __launch_bounds__(fwd_waves(D) * ES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
-           void* __restrict__ O, int B, int E, int tiles_per_head, int outf32) {
+           void* __restrict__ O, int B, int E, int H, int tiles_per_head, int outf32, int n_main, int n_split,
+           int xs, int nct, float* __restrict__ ws) {
   constexpr int NW = fwd_waves(D), NT = NW * 64;  // waves, threads of one E part
   constexpr int KS = D / 16;           // K steps of GEMM1 (= GEMM2 operand count 2 * D/32)
   constexpr int NTN = D / 32;          // N tiles of GEMM2
@@ -65,12 +89,26 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   // row bases then stay in scalar registers (1.5 % faster forward at cfg4 and cfg5s)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
-  const int t = xcd_remap(blockIdx.x, gridDim.x);
-  const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
+  // this workgroup's tile and E-range [cb, ce) of chunks (all of E for a whole tile)
+  const int bid = blockIdx.x;
+  const bool split = bid >= n_main;
+  int cb = 0, ce = (E + 31) >> 5, u = 0;
+  TileId tile;
+  if (!split) {
+    tile = main_tile(xcd_remap(bid, n_main), n_split, H, tiles_per_head);
+  } else {
+    u = bid - n_main;
+    const int s = u / xs;
+    tile = split_tile(s, n_split, H, tiles_per_head);
+    cb = (u - s * xs) * nct;
+    ce = min(ce, cb + nct);
+  }
+  const int h = tile.h, bt = tile.bt;
   // chunks of this part: global chunk c0 + c for c = 0 .. NC - 1 (the last part's last chunks
-  // may lie past E: they load as zeros and add nothing)
-  const int NC = (((E + 31) >> 5) + ES - 1) / ES;
-  const int c0 = part * NC;
+  // may lie past the range: they load as zeros and add nothing)
+  const int NC = (ce - cb + ES - 1) / ES;
+  const int c0 = cb + part * NC;
+  const int e_end = min(E, ce * 32);  // columns of W1 (rows of W2) this workgroup reads
   const unsigned RB = (unsigned)part * FWD_NSLOT * 128u * D;  // this part's ring
 
   const u16* Xh = X + (size_t)h * B * D;
@@ -89,7 +127,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const unsigned dOffW2 = ((tid >> 2) & 31u) * (D * 2u) + (unsigned)(tid >> 7) * 64u + (tid & 3u) * 16u;
   auto dma_chunk = [&](int c) {
     const int cg = c0 + c;
-    const int lim = E - cg * 32;
+    const int lim = e_end - cg * 32;
     const int rem = D * E * 2 - 64 * cg;
     const i32x4 r1 = make_rsrc_words(W1h + (size_t)cg * 32, rem > 0 ? rem : 0);
     const i32x4 r2 = make_rsrc_words(W2h + (size_t)cg * 32 * D, clamp0(lim, 32) * D * 2);
@@ -272,23 +310,131 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
       }
   }
   // ---- epilogue: O tile (C layout: lane = column d, rows 8(i/4) + 4g + i%4); fp32 sums
-  // when the caller asked for them (FMLP_OUT_F32), else rounded to the io dtype ----
-  store_rows<BF16, D>(o, O, (size_t)h * B * D, B, b_wave, g, l32, outf32);
+  // when the caller asked for them (FMLP_OUT_F32), else rounded to the io dtype; a split
+  // tile's partial as fp32 rows of its workspace block ----
+  if (split)
+    store_rows<BF16, D>(o, ws, (size_t)u * BB * D, B - bt * BB, wave * 32, g, l32, 1);
+  else
+    store_rows<BF16, D>(o, O, (size_t)h * B * D, B, b_wave, g, l32, outf32);
+}
+
+// Sum of the split tiles' partials: O rows of split tile s = sum over p < xs of
+// ws[s xs + p] (in p order), fp32 when outf32, else rounded to the io dtype. Four columns per
+// thread; all xs (<= FWD_XS_MAX) partials are loaded before the sum, so their latencies overlap.
+constexpr int FWD_XS_MAX = 16;
+template <bool BF16>
+__global__ void __launch_bounds__(64)
+fwd_reduce_kernel(const float* __restrict__ ws, void* __restrict__ O, int B, int D, int BB, int H, int tiles_per_head,
+                  int xs, int n_split, int outf32) {
+  const int DQ = D >> 2;
+  const long long items = (long long)n_split * BB * DQ;
+  const long long stride = (long long)gridDim.x * blockDim.x;
+  for (long long it = (long long)blockIdx.x * blockDim.x + threadIdx.x; it < items; it += stride) {
+    const int q = (int)(it % DQ);
+    const long long sr = it / DQ;
+    const int r = (int)(sr % BB), s = (int)(sr / BB);
+    const TileId tile = split_tile(s, n_split, H, tiles_per_head);
+    const int h = tile.h, b = tile.bt * BB + r;
+    if (b >= B) continue;
+    const float* src = ws + ((size_t)s * xs * BB + r) * D + 4 * q;
+    float4 v[FWD_XS_MAX];
+#pragma unroll
+    for (int p = 0; p < FWD_XS_MAX; ++p)
+      if (p < xs) v[p] = *(const float4*)(src + (size_t)p * BB * D);
+    float4 acc = v[0];
+#pragma unroll
+    for (int p = 1; p < FWD_XS_MAX; ++p) {
+      if (p < xs) {
+        acc.x += v[p].x;
+        acc.y += v[p].y;
+        acc.z += v[p].z;
+        acc.w += v[p].w;
+      }
+    }
+    const size_t i = ((size_t)h * B + b) * D + 4 * q;
+    if (outf32) {
+      *(float4*)((float*)O + i) = acc;
+    } else {
+      const u32x2 v = {pack2<BF16>(acc.x, acc.y), pack2<BF16>(acc.z, acc.w)};
+      *(u32x2*)((u16*)O + i) = v;
+    }
+  }
 }
 
 // ------------------------------------------------------------------------------------
 // launcher
 // ------------------------------------------------------------------------------------
+// Work split of a forward call on num_cus CUs. Tiles of BB rows (256 at D = 128, 128 at
+// D = 64), R = H ceil(B / BB) of them (at most 2^31 - 1, so every tile index fits an int). One tile per workgroup, one workgroup per CU at a time
+// (D = 128, or D = 64 with the in-workgroup E split) or two (D = 64 without it). A last round
+// of at most N / 4 tiles after full ones (e.g. one ragged tile per head just past a multiple
+// of the CU count) costs nearly as much as a full round, so those tiles are split over E
+// across workgroups, in up to min(N / rem, 16) parts of at least 4 chunks each (two per wave
+// set with the in-workgroup split); the parts' fp32 partials go to the caller's workspace and
+// a second launch sums them. At D = 64 the full round then runs with the in-workgroup split
+// (one tile per CU). Measured on MI355X at H=8 B=4097 D=64 E=2048: 43.9 us unsplit, 33.0 us
+// for the split launch. Small grids (fewer tiles than CUs) gain nothing from it: their tiles'
+// time is mostly fixed latency (12.5 vs 11.4 us at H=12 B=1024 D=64 E=768, before the sum).
+// FMLP_FWD_XS=0 (read once per process) turns the cross-workgroup split off.
+FwdPlan fwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t max_ws) {
+  FwdPlan p{};
+  const long long BB = 2 * D, T = (B + BB - 1) / BB, R = H * T, N = num_cus > 0 ? num_cus : 1;
+  const long long nch = (E + 31) / 32;
+  // in-workgroup split at D = 64 when the tiles fit on the CUs at one workgroup each (the
+  // unsplit kernel would leave a SIMD with one wave) and each part gets at least two chunks;
+  // FMLP_FWD_SPLIT (read once per process): 0 = never, 1 = whenever E allows, else this rule
+  static const int force = env_int("FMLP_FWD_SPLIT", -1);
+  static const int xs_env = env_int("FMLP_FWD_XS", -1);
+  p.es = (D == 64 && E > 64 && (force == 1 || (force != 0 && R <= N))) ? 2 : 1;
+  p.n_main = R;
+  p.xs = 1;
+  p.nct = (int)nch;
+  if (xs_env == 0 || R <= 0) return p;
+  long long cand = 0;
+  int es = p.es;
+  if (R > N) {
+    if (D == 64) {
+      if (R - N <= N / 4 && E > 64 && force != 0) {
+        cand = R - N;
+        es = 2;
+      }
+    } else if (R % N != 0 && R % N <= N / 4) {
+      cand = R % N;
+    }
+  }
+  if (cand <= 0) return p;
+  long long xs = std::min<long long>(std::min<long long>(N / cand, nch / 4), FWD_XS_MAX);
+  if (xs < 2) return p;
+  const long long nct = (nch + xs - 1) / xs;
+  xs = (nch + nct - 1) / nct;
+  const size_t ws = (size_t)cand * (size_t)xs * (size_t)BB * (size_t)D * sizeof(float);
+  if (ws > max_ws || R - cand + cand * xs > 0x7fffffffLL) return p;
+  p.es = es;
+  p.n_main = R - cand;
+  p.n_split = (int)cand;
+  p.xs = (int)xs;
+  p.nct = (int)nct;
+  p.ws_bytes = ws;
+  return p;
+}
+
 template <bool BF16, int D, int ACT, int ES>
-static hipError_t launch_fwd_e(const FwdArgs& a, int tiles_per_head, long long grid, hipStream_t st) {
+static hipError_t launch_fwd_e(const FwdArgs& a, const FwdPlan& p, int tiles_per_head, hipStream_t st) {
   const size_t lds = (size_t)ES * FWD_NSLOT * 128u * D;
   auto k = fwd_kernel<BF16, D, ACT, ES>;
   static std::atomic<unsigned long long> lds_set{0};
   hipError_t e = set_lds_once((const void*)k, (int)lds, lds_set);
   if (e != hipSuccess) return e;
+  const long long grid = p.n_main + (long long)p.n_split * p.xs;
   hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(64 * ES * fwd_waves(D)), lds, st, (const u16*)a.x,
-                     (const u16*)a.w1, (const u16*)a.w2, a.o, (int)a.B, (int)a.E, tiles_per_head,
-                     a.out_f32 ? 1 : 0);
+                     (const u16*)a.w1, (const u16*)a.w2, a.o, (int)a.B, (int)a.E, (int)a.H, tiles_per_head,
+                     a.out_f32 ? 1 : 0, (int)p.n_main, p.n_split, p.xs, p.nct, (float*)a.ws);
+  if ((e = hipGetLastError()) != hipSuccess || p.n_split == 0) return e;
+  constexpr int BB = 32 * fwd_waves(D);
+  const long long items = (long long)p.n_split * BB * (D / 4);
+  const long long blocks = std::min<long long>((items + 63) / 64, 8192);
+  hipLaunchKernelGGL(fwd_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(64), 0, st, (const float*)a.ws, a.o,
+                     (int)a.B, D, BB, (int)a.H, tiles_per_head, p.xs, p.n_split, a.out_f32 ? 1 : 0);
   return hipGetLastError();
 }
 
@@ -299,15 +445,11 @@ static hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   const long long grid = (long long)tiles_per_head * a.H;
   if (grid <= 0) return hipSuccess;
   if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  const FwdPlan p = fwd_plan(a.H, a.B, D, a.E, a.num_cus, a.ws != nullptr ? a.ws_bytes : 0);
   if constexpr (D == 64) {
-    // E split when the tiles fit on the CUs at one workgroup each (the unsplit kernel would
-    // leave a SIMD with one wave) and each part gets at least two chunks.
-    // FMLP_FWD_SPLIT (read once per process): 0 = never, 1 = whenever E allows, else this rule.
-    static const int force = env_int("FMLP_FWD_SPLIT", -1);
-    const bool fits = force == 1 || (force != 0 && grid <= a.num_cus);
-    if (fits && a.E > 64) return launch_fwd_e<BF16, D, ACT, 2>(a, tiles_per_head, grid, st);
+    if (p.es == 2) return launch_fwd_e<BF16, D, ACT, 2>(a, p, tiles_per_head, st);
   }
-  return launch_fwd_e<BF16, D, ACT, 1>(a, tiles_per_head, grid, st);
+  return launch_fwd_e<BF16, D, ACT, 1>(a, p, tiles_per_head, st);
 }
 
 template <bool BF16, int D>

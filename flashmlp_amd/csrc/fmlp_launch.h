@@ -26,7 +26,21 @@ struct FwdArgs {
   int act;
   bool out_f32;  // outputs as fp32 (FMLP_OUT_F32)
   int num_cus;   // compute units of the current device
+  void* ws = nullptr;   // workspace for split tiles' partials (fwd_plan), or none
+  size_t ws_bytes = 0;
 };
+
+// Forward work split (fwd_plan): es = E parts inside a workgroup (1, or 2 at D = 64); tiles
+// 0 .. n_main - 1 run whole, the last n_split tiles each as xs workgroups of nct E-chunks whose
+// fp32 partials take ws_bytes of workspace (0 and n_split = 0 when nothing is split). A split
+// needing more than max_ws bytes is not taken.
+struct FwdPlan {
+  int es;
+  long long n_main;
+  int n_split, xs, nct;
+  size_t ws_bytes;
+};
+FwdPlan fwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t max_ws);
 
 // Backward work decomposition (chosen on the host, see plan_bwd):
 //   dW programs: H * nE * nS, each owning an E-tile of 128 columns and a B-range of

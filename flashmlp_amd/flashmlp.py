@@ -72,6 +72,12 @@ def _ws_bytes(device_index: int, H: int, B: int, D: int, E: int, dtype: int) -> 
     return int(_lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, dtype))
 
 
+@functools.lru_cache(maxsize=256)
+def _fwd_ws_bytes(device_index: int, H: int, B: int, D: int, E: int, dtype: int) -> int:
+    # the forward's split tiles (small grids, a short last round of tiles): fp32 partials
+    return int(_lib.lib().fmlp_fwd_workspace_bytes(H, B, D, E, dtype))
+
+
 def _dense(t: torch.Tensor) -> torch.Tensor:
     # the tuned kernels use 16-byte vector accesses on dense tensors: a strided view, or one at
     # a storage offset that is not a multiple of 16 bytes, is copied
@@ -85,7 +91,7 @@ def _ptr(t):
 
 
 def _alloc_ws(nbytes: int, device: torch.device):
-    # the backward's workspace (None when the plan needs none)
+    # a call's workspace (None when the plan needs none)
     return torch.empty(nbytes, dtype=torch.uint8, device=device) if nbytes else None
 
 
@@ -160,8 +166,13 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
         stream = _stream_of(dev)
         if _tuned(D, E, dtype):
             x, w1, w2 = _dense(x), _dense(w1), _dense(w2)
-            st = L.fmlp_fwd(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), o.data_ptr(), H, B, D, E, dtype,
-                            _act_code(activation), stream)
+            ws_bytes = _fwd_ws_bytes(dev, H, B, D, E, dtype)
+            try:
+                ws = _alloc_ws(ws_bytes, x.device)
+            except torch.OutOfMemoryError:  # the kernels then run every tile whole
+                ws, ws_bytes = None, 0
+            st = L.fmlp_fwd_ws(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), o.data_ptr(), H, B, D, E, dtype,
+                               _act_code(activation), ws.data_ptr() if ws is not None else None, ws_bytes, stream)
         else:
             st = L.fmlp_fwd_strided(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), o.data_ptr(), H, B, D, E,
                                     _lib.strides(x), _lib.strides(w1), _lib.strides(w2), dtype,

@@ -122,6 +122,20 @@ int fmlp_shape_tuned(int64_t D, int64_t E, int dtype);
 int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
              int64_t E, int dtype, int act, void* stream);
 
+/* Bytes of device workspace fmlp_fwd_ws can use for these shapes and dtype on the current
+ * device (0 when the forward needs none). No counterpart in the reference. */
+size_t fmlp_fwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
+
+/* fmlp_fwd with a device workspace (16-byte aligned, or NULL). No counterpart in the reference,
+ * whose forward allocates only o: with at least fmlp_fwd_workspace_bytes() bytes, grids whose
+ * tiles would leave most CUs idle for a round split tiles over E across workgroups. Such grids
+ * are those with fewer tiles than half the CUs, or a short last round after full ones (a ragged
+ * B just past a multiple of the CU count). The parts' fp32 partials go through the workspace
+ * and a second launch sums them in a fixed order. With a smaller workspace or NULL it is
+ * fmlp_fwd. The workspace is scratch for the duration of the call on `stream`. */
+int fmlp_fwd_ws(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
+                int64_t E, int dtype, int act, void* workspace, size_t workspace_bytes, void* stream);
+
 /* fmlp_fwd with X (H,B,D), W1 (H,D,E), W2 (H,E,D) given as strided views: each *_strides is
  * three non-negative element strides (head, row, column); o stays dense. No counterpart in
  * the reference, whose wrapper copies such views through reshape / contiguous
