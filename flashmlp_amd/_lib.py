@@ -47,6 +47,7 @@ SIGNATURES = {
                                    ctypes.c_size_t, _vp]),
     "fmlp_bwd_workspace_bytes": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, ctypes.c_int]),
     "fmlp_bwd_stores_dz": (ctypes.c_int, [_i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int]),
+    "fmlp_bwd_plan": (ctypes.c_int, [_i64, _i64, _i64, _i64, ctypes.c_int, ctypes.c_int, _i64p, ctypes.c_int]),
     "fmlp_bwd": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, ctypes.c_int,
                                 ctypes.c_int, _vp, ctypes.c_size_t, _vp]),
     "fmlp_bwd_strided": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64p, _i64p,
@@ -55,6 +56,7 @@ SIGNATURES = {
                                         ctypes.c_int, _vp]),
 }
 FMLP_SCRATCH_MAX_BYTES = 64 << 20
+ABI_VERSION = 3  # FMLP_ABI_VERSION of include/flashmlp.h
 
 _lock = threading.Lock()
 _lib = None
@@ -78,7 +80,7 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.restype = res
                 fn.argtypes = args
-            if handle.fmlp_abi_version() != 2:
+            if handle.fmlp_abi_version() != ABI_VERSION:
                 raise FlashMLPLibraryError("libflashmlp.so ABI version mismatch; rebuild it")
             _lib = handle
     return _lib

@@ -317,6 +317,22 @@ FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int
   return n;
 }
 
+FMLP_EXPORT int fmlp_bwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, int64_t* info,
+                              int n_info) {
+  int st = check_shape(H, B, D, E, dtype);
+  if (st) return st;
+  if ((st = check_act(act))) return st;
+  if (!tuned_shape(D, E, io_of(dtype))) return fail(FMLP_ERR_UNSUPPORTED, "the generic kernels have no such plan");
+  if (n_info > 0 && info == nullptr) return fail(FMLP_ERR_INVALID_ARG, "info is NULL");
+  int cus = 0;
+  if ((st = num_cus_current(&cus))) return st;
+  const fmlp::BwdPlan p = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus);
+  const int64_t v[10] = {p.dz ? 1 : 0, p.nS, p.dx_es, p.dxs_xs, p.dx_first ? 1 : 0, p.n_dw,
+                         p.n_dx, p.n_dxs, (int64_t)p.ws_bytes, act};
+  for (int i = 0; i < n_info && i < 10; ++i) info[i] = v[i];
+  return ok();
+}
+
 FMLP_EXPORT int fmlp_bwd_stores_dz(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act) {
   if (check_shape(H, B, D, E, dtype) != FMLP_OK || check_act(act) != FMLP_OK) return 0;
   if (!tuned_shape(D, E, io_of(dtype))) return 0;  // the generic kernels recompute

@@ -132,11 +132,13 @@ static_assert(DX_PF <= DX_NSLOT - 2, "a slot is reloaded only after the barrier 
 template <int D, int DES>
 __host__ __device__ constexpr int dx2_rows() { return DX2_ROWS / DES; }
 
+// A program owns tile t's rows and the E-chunks [cb, ce); with pws set (a ragged tile split
+// over E) it stores its fp32 partial dX tile there ([rows][D]) instead of writing dX.
 template <bool BF16, int D, int ACT, int DES = 1>
 __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* __restrict__ W1,
                                          const u16* __restrict__ W2, const u16* __restrict__ dO,
                                          void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32,
-                                         int t) {
+                                         int t, int cb, int ce, float* __restrict__ pws) {
   static_assert(DES == 1 || (DES == 2 && D == 64), "E split");
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr unsigned SLOT = 128u * D;
@@ -153,9 +155,10 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
   const int wp = DES == 1 ? wave : (wave & 3);     // wave within the part
 
   const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
-  const int NC = (E + 31) >> 5;
+  const int NC = ce - cb;
   const int NCP = (NC + DES - 1) / DES;             // chunks per part: global chunk c0 + ci
-  const int c0 = part * NCP;
+  const int c0 = cb + part * NCP;
+  const int e_end = min(E, ce * 32);                // columns of W1 (rows of W2) read
   const int RB = part * DX_NSLOT * (int)SLOT;       // this part's ring
   const bool late = wave >= 4;  // VALU-first half of the workgroup (the second part when split)
 
@@ -183,11 +186,11 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
     }
   }
   // chunk staging: buffer-to-LDS loads DX_PF chunks ahead into a DX_NSLOT-slot ring; part chunk
-  // ci is global chunk c0 + ci, and chunks past the part's share (or past E) load as zeros
+  // ci is global chunk c0 + ci, and chunks past the part's share (or past the range) load as zeros
   auto dma_chunk = [&](int ci) {
     const int c = c0 + ci;
     const bool mine = ci < NCP;
-    const int lim = mine ? E - c * 32 : 0;
+    const int lim = mine ? e_end - c * 32 : 0;
     const int rem = mine ? D * E * 2 - 64 * c : 0;
     const i32x4 r1 = make_rsrc_words(W1h + (size_t)c * 32, rem > 0 ? rem : 0);
     const i32x4 r2 = make_rsrc_words(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
@@ -365,7 +368,10 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
         for (int j = 0; j < 4; ++j) acc[nt][4 * i4 + j] += __uint_as_float(v[j]);
       }
   }
-  store_rows<BF16, D>(acc, dX, (size_t)h * B * D, B, b_wave, g, l32, outf32);
+  if (pws != nullptr)
+    store_rows<BF16, D>(acc, pws, 0, B - bt * dx2_rows<D, DES>(), wp * 32, g, l32, 1);
+  else
+    store_rows<BF16, D>(acc, dX, (size_t)h * B * D, B, b_wave, g, l32, outf32);
 }
 
 // ------------------------------------------------------------------------------------
@@ -693,7 +699,8 @@ template <bool BF16, int D, int ACT, int DES>
 __global__ void __launch_bounds__(DX2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
-  dx2_body<BF16, D, ACT, DES>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32, xcd_remap(blockIdx.x, gridDim.x));
+  dx2_body<BF16, D, ACT, DES>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32, xcd_remap(blockIdx.x, gridDim.x), 0,
+                              (E + 31) >> 5, nullptr);
 }
 
 template <bool BF16, int D, int ACT, bool HILO, bool DZ>
@@ -716,14 +723,27 @@ __global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 
 bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dX, void* __restrict__ dW1, void* __restrict__ dW2,
            float* __restrict__ ws, int H, int B, int E, int nE, int nS, int rows_per_split, int n_dw,
-           int dx_tiles_per_head, int dx_first, int outf32) {
-  const int b = blockIdx.x, n_dx = (int)gridDim.x - n_dw;
+           int dx_tiles_per_head, int dx_first, int outf32, int n_dxs, int dxs_xs, int dxs_nct,
+           float* __restrict__ dxs_ws) {
+  // programs: n_dw dW programs and n_dx whole-tile dX programs (in the plan's order), then
+  // n_dxs = H dxs_xs programs for the heads' ragged last dX tiles split over E (when the plan
+  // splits them, the whole-tile dX programs are the other tiles: T - 1 per head)
+  const int b = blockIdx.x, n_rest = (int)gridDim.x - n_dxs, n_dx = n_rest - n_dw;
+  const int T = dx_tiles_per_head, nch = (E + 31) >> 5;
+  if (b >= n_rest) {
+    const int u = b - n_rest, hh = u / dxs_xs, cb = (u - hh * dxs_xs) * dxs_nct;
+    dx2_body<BF16, D, ACT, DES>(X, W1, W2, dO, dX, B, E, T, outf32, hh * T + T - 1, cb, min(nch, cb + dxs_nct),
+                                dxs_ws + (size_t)u * dx2_rows<D, DES>() * D);
+    return;
+  }
   const int bw = dx_first ? b - n_dx : b;  // index among the dW programs (< 0 or >= n_dw: a dX program)
   if (bw >= 0 && bw < n_dw) {
     dw2_body<BF16, D, ACT, HILO>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32, xcd_remap(bw, n_dw));
   } else {
     const int bx = dx_first ? b : b - n_dw;
-    dx2_body<BF16, D, ACT, DES>(X, W1, W2, dO, dX, B, E, dx_tiles_per_head, outf32, xcd_remap(bx, n_dx));
+    const int m = xcd_remap(bx, n_dx);
+    const int t = n_dxs > 0 ? (m / (T - 1)) * T + m % (T - 1) : m;
+    dx2_body<BF16, D, ACT, DES>(X, W1, W2, dO, dX, B, E, T, outf32, t, 0, nch, nullptr);
   }
 }
 
@@ -1029,11 +1049,23 @@ long long rows_for_split(long long B, long long ns) {
 }
 
 BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int dz_mode, int num_cus,
-                  size_t max_ws, int fixed_des = 0) {
-  // the dX programs' E split follows the default dW mode's plan, so dX does not depend on the
-  // dW mode (FMLP_DW_HILO changes only dW)
-  if (hilo && D == 64 && fixed_des == 0)
-    fixed_des = make_plan(H, B, D, E, act, false, DZ_NEVER, num_cus, max_ws).dx_es;
+                  size_t max_ws) {
+  // Everything that decides how dX is computed (the stored-dZ form or not, the dX programs' E
+  // split, the split of the ragged dX tiles) follows the default dW mode's plan, so dX does not
+  // depend on the dW mode (FMLP_DW_HILO changes only dW).
+  int fixed_des = 0, fixed_dxs = -1, fixed_dz = -1;
+  if (hilo) {
+    const BwdPlan d = make_plan(H, B, D, E, act, false, dz_mode, num_cus, max_ws);
+    fixed_dz = d.dz ? 1 : 0;
+    if (!d.dz) {
+      fixed_des = d.dx_es;
+      fixed_dxs = d.dxs_xs > 0 ? 1 : 0;
+    } else {  // used only if the stored-dZ form does not fit this mode's workspace limit
+      const BwdPlan r = make_plan(H, B, D, E, act, false, DZ_NEVER, num_cus, max_ws);
+      fixed_des = r.dx_es;
+      fixed_dxs = r.dxs_xs > 0 ? 1 : 0;
+    }
+  }
   BwdPlan p{};
   p.nE = (int)((E + DW_ET - 1) / DW_ET);
   const long long base = H * (long long)p.nE, N = num_cus > 0 ? num_cus : 1;
@@ -1057,15 +1089,26 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
   static const int order_env = env_int("FMLP_BWD_ORDER", 0);
   // FMLP_BWD_DXES (read once per process) forces the dX programs' E split (1 or 2, D = 64)
   static const int des_env = env_int("FMLP_BWD_DXES", 0);
+  // Ragged last dX tiles (B not a multiple of the dX rows): one per head, each a whole program
+  // for a few rows, which can leave a last round of H programs on an otherwise idle device. The
+  // plan may split them over E into xs parts of at least 4 chunks (fp32 partials in the
+  // workspace, summed by a second launch); FMLP_BWD_DXSPLIT=0 (read once per process) never does.
+  static const int dxs_env = env_int("FMLP_BWD_DXSPLIT", -1);
+  const long long nch = (E + 31) / 32;
+  long long dxs_xs = std::min<long long>(16, nch / 4);
+  const long long dxs_nct = dxs_xs >= 2 ? (nch + dxs_xs - 1) / dxs_xs : nch;
+  if (dxs_xs >= 2) dxs_xs = (nch + dxs_nct - 1) / dxs_nct;
+  auto dxs_bytes = [&](int des) { return (size_t)H * dxs_xs * (DX2_ROWS / des) * D * sizeof(float); };
   double best_t = 0.0;
   long long best_ns = 1;
-  bool best_dx_first = false;
+  bool best_dx_first = false, best_dxs = false;
   int best_des = 1;
   for (int des = 1; des <= max_des; ++des) {
     if (des_env > 0 && des != des_env) continue;
     if (fixed_des > 0 && des != fixed_des) continue;
-    const long long n_dx = n_dx_for(des);
+    const long long n_dx = n_dx_for(des), T_dx = n_dx / (H > 0 ? H : 1);
     const double tx = tx_for(des);
+    const bool rag = B % (DX2_ROWS / des) != 0 && T_dx >= 2 && dxs_xs >= 2 && dxs_env != 0 && fixed_dxs != 0;
     for (long long ns = 1; ns <= (ns_env > 0 ? 1 : cap); ns *= 2) {
       const long long want = ns_env > 0 ? (ns_env < max_ns ? ns_env : max_ns) : ns;
       const long long rps = rows_for_split(B, want), eff = B > rps ? (B + rps - 1) / rps : 1;
@@ -1073,14 +1116,24 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
       const double tw = kPlanFixedUs + (double)rps * w_per_row;
       const long long n_dw = base * eff;
       const double red = eff > 1 ? kPlanLaunchUs + (double)(2 * eff + 1) * H * E * D * 4.0 / kPlanHbmBytesPerUs : 0.0;
-      for (int o = 1; o <= 2; ++o) {
-        if (order_env && o != order_env) continue;
-        const double t = (o == 1 ? list_makespan(n_dw, tw, n_dx, tx, N) : list_makespan(n_dx, tx, n_dw, tw, N)) + red;
-        if (best_t == 0.0 || t < best_t) {
-          best_t = t;
-          best_ns = eff;
-          best_dx_first = o == 2;
-          best_des = des;
+      const bool dxs_fits = rag && (ws_for(eff) + 255) / 256 * 256 + dxs_bytes(des) <= max_ws;
+      for (int split = 0; split <= 1; ++split) {
+        if (split ? !dxs_fits : fixed_dxs == 1 && dxs_fits) continue;
+        // the split tiles' work, spread over the device, and the launch that sums them
+        const long long nx = split ? n_dx - H : n_dx;
+        const double extra =
+            split ? (double)H * dxs_xs * (kPlanFixedUs + (tx - kPlanFixedUs) / dxs_xs) / N + kPlanLaunchUs : 0.0;
+        for (int o = 1; o <= 2; ++o) {
+          if (order_env && o != order_env) continue;
+          const double t =
+              (o == 1 ? list_makespan(n_dw, tw, nx, tx, N) : list_makespan(nx, tx, n_dw, tw, N)) + red + extra;
+          if (best_t == 0.0 || t < best_t) {
+            best_t = t;
+            best_ns = eff;
+            best_dx_first = o == 2;
+            best_des = des;
+            best_dxs = split == 1;
+          }
         }
       }
     }
@@ -1088,6 +1141,11 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
   p.dx_es = best_des;
   p.dx_tiles_per_head = (int)((B + DX2_ROWS / best_des - 1) / (DX2_ROWS / best_des));
   p.n_dx = (long long)p.dx_tiles_per_head * H;
+  if (best_dxs) {
+    p.dxs_xs = (int)dxs_xs;
+    p.dxs_nct = (int)dxs_nct;
+    p.n_dx -= H;
+  }
   // Stored-dZ form: the dW launch alone (programs dealt over the CUs) and its reduction, then
   // storing dZ and streaming it back through the dX GEMM (memory-bound: a rate per byte, in the
   // same time units, and a fixed part for the extra launch). Fitted to the same-box times of
@@ -1115,12 +1173,14 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
       }
     }
   }
-  p.dz = best_dz > 0.0 && (dz_want == 1 || best_dz < best_t);
+  p.dz = best_dz > 0.0 && (fixed_dz >= 0 ? fixed_dz == 1 : (dz_want == 1 || best_dz < best_t));
   if (p.dz) {
     best_ns = best_dz_ns;
     best_dx_first = false;
     p.dx_es = 1;
     p.dx_tiles_per_head = (int)((B + DX2_ROWS - 1) / DX2_ROWS);
+    p.dxs_xs = 0;
+    p.dxs_nct = 0;
   }
   const long long rps = rows_for_split(B, best_ns);
   p.nS = (int)(B > rps ? (B + rps - 1) / rps : 1);
@@ -1128,6 +1188,11 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
   p.n_dw = base * p.nS;
   p.dx_first = best_dx_first;
   p.ws_bytes = ws_for(p.nS);
+  if (p.dxs_xs > 0) {  // the split dX tiles' partials after the dW partials
+    p.n_dxs = H * (long long)p.dxs_xs;
+    p.dxs_off = (p.ws_bytes + 255) / 256 * 256;
+    p.ws_bytes = p.dxs_off + dxs_bytes(p.dx_es);
+  }
   if (p.dz) {
     p.Bp = (int)Bp;
     p.dz_off = (p.ws_bytes + 255) / 256 * 256;
@@ -1173,7 +1238,8 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo,
 
 template <bool BF16, int D, int ACT, int DES>
 static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
-  if (p.n_dw > 0x7fffffffLL || p.n_dx > 0x7fffffffLL || p.n_dw + p.n_dx > 0x7fffffffLL) return hipErrorInvalidValue;
+  if (p.n_dw + p.n_dx + p.n_dxs > 0x7fffffffLL || (long long)p.dx_tiles_per_head * a.H > 0x7fffffffLL)
+    return hipErrorInvalidValue;
   hipError_t e;
   // the dW role's: two weight tiles and three subtile pairs (256 D bytes each); at least the
   // dX role's rings (one or two parts of DX_NSLOT slots of 128 D bytes)
@@ -1214,20 +1280,25 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   // 0 = dW programs (and their reduction), then dX programs, as separate launches
   static const int unified = env_int("FMLP_BWD_UNIFIED", 1);
   // a partial backward (FMLP_BWD_NO_DX / FMLP_BWD_NO_DW) launches only the programs it needs
-  if (unified && a.want_dx && a.want_dw && p.n_dw > 0 && p.n_dx > 0) {
+  if (unified && a.want_dx && a.want_dw && p.n_dw > 0 && p.n_dx + p.n_dxs > 0) {
+    float* dxs_ws = p.n_dxs > 0 ? (float*)((char*)a.ws + p.dxs_off) : nullptr;
     auto launch_u = [&](auto k) {
       static std::atomic<unsigned long long> lds_set{0};
       hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
       if (r != hipSuccess) return r;
-      hipLaunchKernelGGL(k, dim3((unsigned)(p.n_dw + p.n_dx)), dim3(DW2_NT), lds, st, (const u16*)a.x,
+      hipLaunchKernelGGL(k, dim3((unsigned)(p.n_dw + p.n_dx + p.n_dxs)), dim3(DW2_NT), lds, st, (const u16*)a.x,
                          (const u16*)a.w1, (const u16*)a.w2, (const u16*)a.dout, a.dx, a.dw1, a.dw2, (float*)a.ws,
                          (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw,
-                         p.dx_tiles_per_head, p.dx_first ? 1 : 0, a.out_f32 ? 1 : 0);
+                         p.dx_tiles_per_head, p.dx_first ? 1 : 0, a.out_f32 ? 1 : 0, (int)p.n_dxs, p.dxs_xs,
+                         p.dxs_nct, dxs_ws);
       return hipGetLastError();
     };
     e = a.dw_hilo ? launch_u(bwd_kernel<BF16, D, ACT, true, DES>) : launch_u(bwd_kernel<BF16, D, ACT, false, DES>);
     if (e != hipSuccess) return e;
-    return reduce();
+    if ((e = reduce()) != hipSuccess || p.n_dxs == 0) return e;
+    // the ragged dX tiles' partials: split tile s is head s's last tile
+    return launch_tile_reduce(dxs_ws, a.dx, BF16, (int)a.B, D, DX2_ROWS / DES, (int)a.H, p.dx_tiles_per_head,
+                              p.dxs_xs, (int)a.H, a.out_f32 ? 1 : 0, st);
   }
   if (p.n_dw > 0 && a.want_dw) {
     auto launch_w = [&](auto k) {
@@ -1243,13 +1314,14 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     if (e != hipSuccess) return e;
     if ((e = reduce()) != hipSuccess) return e;
   }
-  if (p.n_dx > 0 && a.want_dx) {
+  const long long n_dx_all = (long long)p.dx_tiles_per_head * a.H;  // whole tiles only here
+  if (n_dx_all > 0 && a.want_dx) {
     const size_t lds_x = (size_t)DES * DX_NSLOT * 128u * D;  // the chunk ring(s)
     auto k = dx2_kernel<BF16, D, ACT, DES>;
     static std::atomic<unsigned long long> lds_set{0};
     e = set_lds_once((const void*)k, (int)lds_x, lds_set);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(k, dim3((unsigned)p.n_dx), dim3(DX2_NT), lds_x, st, (const u16*)a.x, (const u16*)a.w1,
+    hipLaunchKernelGGL(k, dim3((unsigned)n_dx_all), dim3(DX2_NT), lds_x, st, (const u16*)a.x, (const u16*)a.w1,
                        (const u16*)a.w2, (const u16*)a.dout, a.dx, (int)a.B, (int)a.E, p.dx_tiles_per_head,
                        a.out_f32 ? 1 : 0);
     if ((e = hipGetLastError()) != hipSuccess) return e;

@@ -430,11 +430,22 @@ static hipError_t launch_fwd_e(const FwdArgs& a, const FwdPlan& p, int tiles_per
                      (const u16*)a.w1, (const u16*)a.w2, a.o, (int)a.B, (int)a.E, (int)a.H, tiles_per_head,
                      a.out_f32 ? 1 : 0, (int)p.n_main, p.n_split, p.xs, p.nct, (float*)a.ws);
   if ((e = hipGetLastError()) != hipSuccess || p.n_split == 0) return e;
-  constexpr int BB = 32 * fwd_waves(D);
-  const long long items = (long long)p.n_split * BB * (D / 4);
+  return launch_tile_reduce((const float*)a.ws, a.o, BF16, (int)a.B, D, 32 * fwd_waves(D), (int)a.H, tiles_per_head,
+                            p.xs, p.n_split, a.out_f32 ? 1 : 0, st);
+}
+
+hipError_t launch_tile_reduce(const float* ws, void* out, bool bf16, int B, int D, int BB, int H, int T, int xs,
+                              int n_split, int outf32, hipStream_t st) {
+  if (xs < 1 || xs > FWD_XS_MAX || D % 4 != 0) return hipErrorInvalidValue;
+  const long long items = (long long)n_split * BB * (D / 4);
   const long long blocks = std::min<long long>((items + 63) / 64, 8192);
-  hipLaunchKernelGGL(fwd_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(64), 0, st, (const float*)a.ws, a.o,
-                     (int)a.B, D, BB, (int)a.H, tiles_per_head, p.xs, p.n_split, a.out_f32 ? 1 : 0);
+  if (blocks <= 0) return hipSuccess;
+  if (bf16)
+    hipLaunchKernelGGL(fwd_reduce_kernel<true>, dim3((unsigned)blocks), dim3(64), 0, st, ws, out, B, D, BB, H, T, xs,
+                       n_split, outf32);
+  else
+    hipLaunchKernelGGL(fwd_reduce_kernel<false>, dim3((unsigned)blocks), dim3(64), 0, st, ws, out, B, D, BB, H, T,
+                       xs, n_split, outf32);
   return hipGetLastError();
 }
 

@@ -55,8 +55,12 @@ struct BwdPlan {
   int rows_per_split;  // multiple of 32
   int dx_tiles_per_head;
   int dx_es;           // dX programs: 1 = 256 rows, all E-chunks; 2 = 128 rows, E in two parts (D = 64)
+  int dxs_xs, dxs_nct; // ragged last dX tiles (one per head) split over E: parts and chunks per
+                       // part (0: not split; single-launch recompute form only)
+  long long n_dxs;     // programs of the split tiles (H dxs_xs)
+  size_t dxs_off;      // byte offset of their fp32 partials ([H][dxs_xs][rows][D]) in the workspace
   bool dx_first;       // single-launch order: dX programs before the dW programs
-  long long n_dw, n_dx;
+  long long n_dw, n_dx;  // dW programs, whole-tile dX programs
   bool dz;             // stored-dZ form
   int Bp;              // B rounded up to 256 (dZ tiles), stored-dZ form
   int n_xg;            // dxg_kernel workgroups (persistent), stored-dZ form
@@ -135,6 +139,12 @@ enum { DZ_NEVER = 0, DZ_AUTO = 1, DZ_FORCE = 2 };
 BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo, int dz_mode, int num_cus,
                  size_t max_ws = (size_t)-1);
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t st);
+// Sum of split tiles' fp32 partials (fmlp_fwd.hip): tiles of BB rows, T per head; split tile s
+// (of n_split, the last n_split in row-block-major order) has xs partial [BB][D] blocks at
+// ws + (s xs + p) BB D; its rows (< B) of `out` (H, B, D) get their sum in p order, rounded to
+// the io dtype (bf16 or fp16) or fp32 when outf32.
+hipError_t launch_tile_reduce(const float* ws, void* out, bool bf16, int B, int D, int BB, int H, int T, int xs,
+                              int n_split, int outf32, hipStream_t st);
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st);
 
 // The library's static device scratch (fmlp_bwd_noalloc): its device address on the current

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define FMLP_ABI_VERSION 2  /* 2: FMLP_BWD_NO_DX / FMLP_BWD_NO_DW */
+#define FMLP_ABI_VERSION 3  /* 2: FMLP_BWD_NO_DX / FMLP_BWD_NO_DW; 3: fmlp_fwd_ws, fmlp_bwd_plan */
 
 typedef enum {
   FMLP_OK = 0,
@@ -127,12 +127,12 @@ int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o, int64_t H, 
 size_t fmlp_fwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
 /* fmlp_fwd with a device workspace (16-byte aligned, or NULL). No counterpart in the reference,
- * whose forward allocates only o: with at least fmlp_fwd_workspace_bytes() bytes, grids whose
- * tiles would leave most CUs idle for a round split tiles over E across workgroups. Such grids
- * are those with fewer tiles than half the CUs, or a short last round after full ones (a ragged
- * B just past a multiple of the CU count). The parts' fp32 partials go through the workspace
- * and a second launch sums them in a fixed order. With a smaller workspace or NULL it is
- * fmlp_fwd. The workspace is scratch for the duration of the call on `stream`. */
+ * whose forward allocates only o: with at least fmlp_fwd_workspace_bytes() bytes, a grid whose
+ * last round of tiles would leave most CUs idle (a short last round after full ones, e.g. a
+ * ragged B just past a multiple of the CU count) splits those tiles over E across workgroups.
+ * The parts' fp32 partials go through the workspace and a second launch sums them in a fixed
+ * order. With a smaller workspace or NULL it is fmlp_fwd. The workspace is scratch for the
+ * duration of the call on `stream`. */
 int fmlp_fwd_ws(const void* x, const void* w1, const void* w2, void* o, int64_t H, int64_t B, int64_t D,
                 int64_t E, int dtype, int act, void* workspace, size_t workspace_bytes, void* stream);
 
@@ -158,6 +158,15 @@ size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int 
  * current device, else 0 (also for rejected arguments). No counterpart in the reference: for
  * callers planning memory and for benches naming the kernels they time. */
 int fmlp_bwd_stores_dz(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act);
+
+/* The tuned backward's plan for these shapes, dtype flags and activation on the current
+ * device, written to info[0 .. n_info - 1] (at most 10 values, in this order): stored-dZ form
+ * (0/1), B splits of the dW programs, dX programs' in-workgroup E parts, parts of each split
+ * ragged dX tile (0: not split), dX programs first (0/1), dW programs, whole-tile dX programs,
+ * split-tile dX programs, workspace bytes, and the activation's code. Returns FMLP_OK, or
+ * FMLP_ERR_UNSUPPORTED for shapes the tuned kernels do not take. No counterpart in the
+ * reference: a diagnostic for tests and benches. */
+int fmlp_bwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, int64_t* info, int n_info);
 
 /*
  * Backward: dx = dZ @ w1^T, dw1 = x^T @ dZ, dw2 = h^T @ dout with h = act(x @ w1),
