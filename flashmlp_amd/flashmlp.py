@@ -112,32 +112,31 @@ def _stream_of(index: int) -> int:
     return torch.cuda.current_stream(index).cuda_stream
 
 
-class _OnDevice:
-    """Makes `index` the current device for the C ABI call (the library launches on the current
-    device) only when it is not already; restores the previous one afterwards."""
-
-    __slots__ = ("index", "prev")
-
-    def __init__(self, index: int):
-        self.index = index
-        self.prev = None
-
-    def __enter__(self):
-        cur = _get_device() if _get_device is not None else torch.cuda.current_device()
-        if cur != self.index:
-            self.prev = cur
-            torch.cuda.set_device(self.index)
-        return self
-
-    def __exit__(self, *exc):
-        if self.prev is not None:
-            torch.cuda.set_device(self.prev)
-        return False
+def _io_code(x: torch.Tensor, *ts: torch.Tensor):
+    """The io dtype code when every tensor is a GPU tensor of x's dtype on x's device (the common
+    case, checked with the cheapest accessors), else the reason raised by _check_tensors."""
+    dt = x.dtype
+    d = x.get_device()
+    code = _DTYPES.get(dt)
+    if d < 0 or code is None or any(t.dtype is not dt or t.get_device() != d for t in ts):
+        return _check_tensors(x, *ts)
+    return code
 
 
-def _index(t: torch.Tensor) -> int:
-    i = t.device.index
-    return i if i is not None else torch.cuda.current_device()
+def _dense_all(*ts: torch.Tensor):
+    # the tuned kernels' inputs: unchanged when all are dense and 16-byte aligned
+    if all(t.is_contiguous() and t.data_ptr() % 16 == 0 for t in ts):
+        return ts
+    return tuple(_dense(t) for t in ts)
+
+
+def _empty_as(t: torch.Tensor, shape) -> torch.Tensor:
+    # a dense output of t's shape, dtype and device (empty_like is the cheapest allocation)
+    return torch.empty_like(t) if t.is_contiguous() else t.new_empty(shape)
+
+
+def _current_device() -> int:
+    return _get_device() if _get_device is not None else torch.cuda.current_device()
 
 
 def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation: str = "") -> torch.Tensor:
@@ -158,14 +157,17 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
     assert E == E2, "Intermediate dimension mismatch"
     assert D == D2, "Output dimension mismatch"
 
-    dtype = _check_tensors(x, w1, w2)
-    o = torch.empty((H, B, D), dtype=x.dtype, device=x.device)
+    dtype = _io_code(x, w1, w2)
+    o = _empty_as(x, (H, B, D))
     L = _lib.lib()
-    dev = _index(x)
-    with _OnDevice(dev):
+    dev = x.get_device()
+    prev = _current_device()
+    if prev != dev:  # the library launches on the current device
+        torch.cuda.set_device(dev)
+    try:
         stream = _stream_of(dev)
         if _tuned(D, E, dtype):
-            x, w1, w2 = _dense(x), _dense(w1), _dense(w2)
+            x, w1, w2 = _dense_all(x, w1, w2)
             ws_bytes = _fwd_ws_bytes(dev, H, B, D, E, dtype)
             try:
                 ws = _alloc_ws(ws_bytes, x.device)
@@ -177,6 +179,9 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
             st = L.fmlp_fwd_strided(x.data_ptr(), w1.data_ptr(), w2.data_ptr(), o.data_ptr(), H, B, D, E,
                                     _lib.strides(x), _lib.strides(w1), _lib.strides(w2), dtype,
                                     _act_code(activation), stream)
+    finally:
+        if prev != dev:
+            torch.cuda.set_device(prev)
     _lib.check(st, "forward")
     return o
 
@@ -206,21 +211,25 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     assert D == D2, "Output dimension mismatch"
     assert x.shape == do.shape, "Gradient shape mismatch"
 
-    dtype = _check_tensors(x, w1, w2, do)
+    dtype = _io_code(x, w1, w2, do)
     need_dx, need_dw = bool(_needs[0]), bool(_needs[1])
     flags = dtype | (_lib.FMLP_DW_HILO if accurate_dw else 0) | (_lib.FMLP_BWD_RECOMPUTE if recompute else 0)
-    flags |= (0 if need_dx else _lib.FMLP_BWD_NO_DX) | (0 if need_dw else _lib.FMLP_BWD_NO_DW)
-    dx = torch.empty((H, B, D), dtype=x.dtype, device=x.device) if need_dx else None
-    dw1 = torch.empty((H, D, E), dtype=x.dtype, device=x.device) if need_dw else None
-    dw2 = torch.empty((H, E, D), dtype=x.dtype, device=x.device) if need_dw else None
+    if not (need_dx and need_dw):
+        flags |= (0 if need_dx else _lib.FMLP_BWD_NO_DX) | (0 if need_dw else _lib.FMLP_BWD_NO_DW)
+    dx = _empty_as(x, (H, B, D)) if need_dx else None
+    dw1 = _empty_as(w1, (H, D, E)) if need_dw else None
+    dw2 = _empty_as(w2, (H, E, D)) if need_dw else None
     if not (need_dx or need_dw):
         return dx, dw1, dw2
     L = _lib.lib()
-    dev = _index(x)
-    with _OnDevice(dev):
+    dev = x.get_device()
+    prev = _current_device()
+    if prev != dev:  # the library launches on the current device
+        torch.cuda.set_device(dev)
+    try:
         stream = _stream_of(dev)
         if _tuned(D, E, dtype):
-            x, w1, w2, do = _dense(x), _dense(w1), _dense(w2), _dense(do)
+            x, w1, w2, do = _dense_all(x, w1, w2, do)
             ws_bytes = _ws_bytes(dev, H, B, D, E, flags)
             try:
                 ws = _alloc_ws(ws_bytes, x.device)
@@ -247,6 +256,9 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
                                     _ptr(dw1), _ptr(dw2), H, B, D, E, _lib.strides(x), _lib.strides(w1),
                                     _lib.strides(w2), _lib.strides(do), flags, _act_code(activation),
                                     ws.data_ptr() if ws is not None else None, ws_bytes, stream)
+    finally:
+        if prev != dev:
+            torch.cuda.set_device(prev)
     _lib.check(st, "backward")
     return dx, dw1, dw2
 
