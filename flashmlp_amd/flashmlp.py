@@ -41,6 +41,11 @@ import torch
 
 from . import _lib
 
+try:  # the per-call fast path over the same C ABI (fmlp_py.cpp); the ctypes path otherwise
+    from . import _fmlp_fast as _fast
+except ImportError:
+    _fast = None
+
 _DTYPES = {torch.float16: _lib.FMLP_DTYPE_F16, torch.bfloat16: _lib.FMLP_DTYPE_BF16,
            torch.float32: _lib.FMLP_DTYPE_F32}
 
@@ -157,6 +162,11 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
     assert E == E2, "Intermediate dimension mismatch"
     assert D == D2, "Output dimension mismatch"
 
+    if _fast is not None:  # 16-bit, one GPU, dense and aligned, a tuned shape: else None
+        r = _fast.fwd(x, w1, w2, _act_code(activation))
+        if r is not None:
+            _lib.check(r[0], "forward")
+            return r[1]
     dtype = _io_code(x, w1, w2)
     o = _empty_as(x, (H, B, D))
     L = _lib.lib()
@@ -211,11 +221,17 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     assert D == D2, "Output dimension mismatch"
     assert x.shape == do.shape, "Gradient shape mismatch"
 
-    dtype = _io_code(x, w1, w2, do)
     need_dx, need_dw = bool(_needs[0]), bool(_needs[1])
-    flags = dtype | (_lib.FMLP_DW_HILO if accurate_dw else 0) | (_lib.FMLP_BWD_RECOMPUTE if recompute else 0)
+    flags = (_lib.FMLP_DW_HILO if accurate_dw else 0) | (_lib.FMLP_BWD_RECOMPUTE if recompute else 0)
     if not (need_dx and need_dw):
         flags |= (0 if need_dx else _lib.FMLP_BWD_NO_DX) | (0 if need_dw else _lib.FMLP_BWD_NO_DW)
+    if _fast is not None and (need_dx or need_dw):  # as in flashmlp_fwd
+        r = _fast.bwd(x, w1, w2, do, _act_code(activation), flags)
+        if r is not None:
+            _lib.check(r[0], "backward")
+            return r[1], r[2], r[3]
+    dtype = _io_code(x, w1, w2, do)
+    flags |= dtype
     dx = _empty_as(x, (H, B, D)) if need_dx else None
     dw1 = _empty_as(w1, (H, D, E)) if need_dw else None
     dw2 = _empty_as(w2, (H, E, D)) if need_dw else None

@@ -47,6 +47,22 @@ def test_no_cpu_fallback():
         fm.FlashMLPFunction.apply(x, w1, w2, "silu")
 
 
+def test_fast_path_declines_what_it_does_not_take():
+    """The wrappers' fast path (_fmlp_fast, built with the library) returns None for anything but
+    16-bit GPU tensors of a tuned shape, so the general path validates and raises."""
+    import importlib
+
+    fmm = importlib.import_module("flashmlp_amd.flashmlp")
+    assert fmm._fast is not None, "_fmlp_fast.so is not built"
+    x, w1, w2, do = make_inputs(2, 16, 64, 64, torch.bfloat16)
+    assert fmm._fast.fwd(x, w1, w2, 1) is None
+    assert fmm._fast.bwd(x, w1, w2, do, 1, 0) is None
+    assert fmm._fast.fwd(x.float(), w1.float(), w2.float(), 1) is None
+    assert fmm._fast.fwd(x, w1, "not a tensor", 1) is None
+    with pytest.raises(TypeError):
+        fmm._fast.fwd(x, w1, w2)
+
+
 def test_module_parameters_match_reference_layout():
     # flashmlp.py:577-591: parameter names, shapes, dtype and init scales
     torch.manual_seed(0)

@@ -176,11 +176,88 @@ def test_bwd_falls_back_to_recompute_when_workspace_does_not_fit(monkeypatch):
         return real(nbytes, device)
 
     monkeypatch.setattr(fmm, "_alloc_ws", tight)
+    monkeypatch.setattr(fmm, "_fast", None)  # the general path (the fast path allocates in C++)
     got = fm.flashmlp_bwd(x, w1, w2, do, act)
     torch.cuda.synchronize()
     assert len(sizes) == 2 and sizes[0] > (64 << 20) >= sizes[1]
     for a, b in zip(got, ref):
         assert torch.equal(a, b)
+
+
+def test_fast_path_falls_back_to_recompute_when_workspace_does_not_fit():
+    """The fast path (_fmlp_fast) takes the recompute form when allocating the stored-dZ
+    workspace fails, like the general path: a real allocation failure under a per-process memory
+    limit that leaves room for the outputs and the recompute form's workspace only."""
+    import importlib
+
+    from flashmlp_amd import _lib
+
+    fmm = importlib.import_module("flashmlp_amd.flashmlp")
+    assert fmm._fast is not None, "the fast path module is not built"
+    dt, act = torch.bfloat16, "silu"
+    code, act_code = _lib.FMLP_DTYPE_BF16, _lib.ACT_CODES[act]
+    L = _lib.lib()
+    found = None
+    for H, B, D, E in [(16, 8192, 128, 1024), (32, 8192, 128, 1024), (32, 16384, 128, 1024)]:
+        if L.fmlp_bwd_stores_dz(H, B, D, E, code, act_code) != 1:
+            continue
+        dz_ws = L.fmlp_bwd_workspace_bytes(H, B, D, E, code)
+        rec_ws = L.fmlp_bwd_workspace_bytes(H, B, D, E, code | _lib.FMLP_BWD_RECOMPUTE)
+        out = 2 * (H * B * D + 2 * H * D * E)
+        if dz_ws > rec_ws + out + (96 << 20):
+            found = (H, B, D, E, rec_ws, out)
+            break
+    assert found, "no candidate shape takes the stored-dZ form with room to tell the forms apart"
+    H, B, D, E, rec_ws, out = found
+    _say(f"[api] fast-path workspace fallback H={H} B={B} D={D} E={E} {dt} act='{act}'")
+    x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=62))
+    ref = fm.flashmlp_bwd(x, w1, w2, do, act, recompute=True)
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    total = torch.cuda.get_device_properties(0).total_memory
+    allowed = torch.cuda.memory_reserved() + rec_ws + out + (64 << 20)
+    torch.cuda.set_per_process_memory_fraction(allowed / total)
+    try:
+        got = fm.flashmlp_bwd(x, w1, w2, do, act)
+        torch.cuda.synchronize()
+    finally:
+        torch.cuda.set_per_process_memory_fraction(1.0)
+    for a, b in zip(got, ref):
+        assert torch.equal(a, b)
+
+
+FAST_CASES = [
+    (4, 1000, 64, 512, torch.float16, "sigmoid"),       # tuned, B tail
+    (8, 4097, 64, 2048, torch.float16, "sigmoid"),      # forward split tiles, ragged dX split
+    (2, 4096, 128, 512, torch.bfloat16, "silu"),        # B split of the dW programs
+    (4, 2048, 128, 1024, torch.bfloat16, "leaky_relu"),
+]
+
+
+@pytest.mark.parametrize("H,B,D,E,dt,act", FAST_CASES, ids=[f"H{c[0]}-B{c[1]}-D{c[2]}-E{c[3]}" for c in FAST_CASES])
+def test_fast_path_equals_general_path(monkeypatch, H, B, D, E, dt, act):
+    """flashmlp_fwd / flashmlp_bwd through _fmlp_fast and through the ctypes path give bitwise
+    equal results (the same C ABI calls), for every backward mode and partial backward."""
+    import importlib
+
+    fmm = importlib.import_module("flashmlp_amd.flashmlp")
+    assert fmm._fast is not None, "the fast path module is not built"
+    _say(f"[api] fast vs general H={H} B={B} D={D} E={E} {dt} act='{act}'")
+    x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=63))
+    kws = [dict(), dict(recompute=True), dict(accurate_dw=True), dict(_needs=(True, False)),
+           dict(_needs=(False, True))]
+    fast_o = fm.flashmlp_fwd(x, w1, w2, act)
+    fast_g = [fm.flashmlp_bwd(x, w1, w2, do, act, **kw) for kw in kws]
+    monkeypatch.setattr(fmm, "_fast", None)
+    gen_o = fm.flashmlp_fwd(x, w1, w2, act)
+    gen_g = [fm.flashmlp_bwd(x, w1, w2, do, act, **kw) for kw in kws]
+    torch.cuda.synchronize()
+    assert torch.equal(fast_o, gen_o)
+    for kw, a, b in zip(kws, fast_g, gen_g):
+        for u, v in zip(a, b):
+            assert (u is None) == (v is None), kw
+            if u is not None:
+                assert torch.equal(u, v), kw
 
 
 @pytest.mark.parametrize("H,B,D,E,dt,act", [
