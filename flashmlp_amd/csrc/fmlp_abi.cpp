@@ -327,9 +327,9 @@ FMLP_EXPORT int fmlp_bwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int dt
   int cus = 0;
   if ((st = num_cus_current(&cus))) return st;
   const fmlp::BwdPlan p = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus);
-  const int64_t v[10] = {p.dz ? 1 : 0, p.nS, p.dx_es, p.dxs_xs, p.dx_first ? 1 : 0, p.n_dw,
-                         p.n_dx, p.n_dxs, (int64_t)p.ws_bytes, act};
-  for (int i = 0; i < n_info && i < 10; ++i) info[i] = v[i];
+  const int64_t v[11] = {p.dz ? 1 : 0, p.nS, p.dx_es, p.dxs_xs, p.dx_first ? 1 : 0, p.n_dw,
+                         p.n_dx, p.n_dxs, (int64_t)p.ws_bytes, act, p.et_w};
+  for (int i = 0; i < n_info && i < 11; ++i) info[i] = v[i];
   return ok();
 }
 

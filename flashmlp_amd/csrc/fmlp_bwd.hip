@@ -393,8 +393,10 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
 constexpr int DW2_NW = 8;
 constexpr int DW2_NT = DW2_NW * 64;
 
+// weight tile of ET rows: D/32 blocks of [ET rows][64 bytes]
+template <int ET>
 __device__ __forceinline__ unsigned wt_off(unsigned r, unsigned q) {
-  return (q >> 2) * 8192u + r * 64u + (((q & 3u) ^ ((r >> 2) & 3u)) << 4);
+  return (q >> 2) * (ET * 64u) + r * 64u + (((q & 3u) ^ ((r >> 2) & 3u)) << 4);
 }
 
 // HILO: the dW products take h and dZ as two io-dtype terms, hi = round(v) and
@@ -405,37 +407,47 @@ __device__ __forceinline__ unsigned wt_off(unsigned r, unsigned q) {
 // dxg_kernel streams into LDS: [h][b / 256][e / 32][(b % 256) / 32][e % 32][32 positions], row
 // b at position sig(b % 32) (bits 2 and 3 swapped), so each 32-column chunk of a 256-row tile
 // is 16 contiguous KB.
-template <bool BF16, int D, int ACT, bool HILO, bool DZ = false>
+// ET: E-columns per program, 128 (four column groups of waves, two row sets: the form
+// described above) or 64 (D = 64, recompute form only: two column groups, four row sets, wave
+// w taking every fourth subtile of its set; twice the programs, each half the work, for grids
+// that leave CUs idle). Waves w and w + 4 share a SIMD; their sets differ by RS / 2, so one
+// runs the schedule half a group behind the other either way.
+template <bool BF16, int D, int ACT, bool HILO, bool DZ = false, int ET = DW_ET>
 __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* __restrict__ W1,
                                          const u16* __restrict__ W2, const u16* __restrict__ dO,
                                          void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
                                          int H, int B, int E, int nE, int nS, int rows_per_split, int outf32,
                                          int t, u16* __restrict__ dzt = nullptr, int Bp = 0) {
+  static_assert(ET == DW_ET || (ET == 64 && D == 64 && !DZ), "E-tile width");
   constexpr int KS = D / 16, NTN = D / 32;
+  constexpr int CG = ET / 32;            // column groups of waves
+  constexpr int RS = DW2_NW / CG;        // row sets (a set takes every RS-th subtile)
   constexpr int SUB = 64 * D;            // bytes of a [32][D] subtile
-  constexpr int PAIR = 4 * SUB;          // X set0, dO set0, X set1, dO set1
-  constexpr int WT = 256 * D;            // bytes of a [128][D] weight tile
+  constexpr int PAIR = 2 * RS * SUB;     // a group of subtiles: X set0, dO set0, X set1, dO set1, ...
+  constexpr int WT = 2 * ET * D;         // bytes of an [ET][D] weight tile
+  constexpr int WTB = ET * 64;           // bytes of one 32-column block of it
   // ring first (its runtime slot base plus constant offsets stays within the 16-bit DS
   // immediate range), weight tiles above it (addressed from a lane register that holds
   // the tile base)
   constexpr int RING_OFF = 0, W1T_OFF = 3 * PAIR, W2T_OFF = W1T_OFF + WT;
-  constexpr int NPL = PAIR / 16 / DW2_NT;  // 16-byte pieces per lane per pair
+  constexpr int NPL = PAIR / 16 / DW2_NT;  // 16-byte pieces per lane per group
+  static_assert(PAIR % (16 * DW2_NT) == 0 && (ET * D / 8) % DW2_NT == 0, "piece counts");
   constexpr int N1 = 2 * KS, N2 = 4 * NTN;
   constexpr int PD = 2;
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
-  const int cg = wave & 3, set = wave >> 2;
+  const int cg = wave % CG, set = wave / CG;
   const int et = t % nE;
   const int hs = t / nE;
   const int s = hs % nS, h = hs / nS;
-  const int e_prog = et * DW_ET;
+  const int e_prog = et * ET;
   const int e0 = e_prog + 32 * cg;
   const int b_lo = s * rows_per_split;
   const int b_hi = min(B, b_lo + rows_per_split);
   const int nsub = (b_hi - b_lo + DW_BT - 1) / DW_BT;
-  const int npair = (nsub + 1) >> 1;
+  const int npair = (nsub + RS - 1) / RS;
 
   const u16* Xh = X + (size_t)h * B * D;
   const u16* dOh = dO + (size_t)h * B * D;
@@ -444,22 +456,22 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
 
   // ---- weight tiles (once): W2T rows natural, W1T transposed with 2-byte writes ----
 #pragma unroll
-  for (int k = 0; k < D / 32; ++k) {
+  for (int k = 0; k < ET * D / 8 / DW2_NT; ++k) {
     const int p = tid + k * DW2_NT;
     {  // W2 row e_prog + r, piece q
       const int r = p / (D / 8), q = p % (D / 8);
       u32x4 v = {0u, 0u, 0u, 0u};
       if (e_prog + r < E) v = *(const u32x4*)(W2h + (size_t)(e_prog + r) * D + q * 8);
-      lds_write16(W2T_OFF + (int)wt_off(r, q), v);
+      lds_write16(W2T_OFF + (int)wt_off<ET>(r, q), v);
     }
     {  // W1 row d, columns e_prog + 8u .. + 7  ->  W1T rows 8u + j, column d
-      const int d = p >> 4, u = p & 15;
+      const int d = p / (ET / 8), u = p % (ET / 8);
       u32x4 v = {0u, 0u, 0u, 0u};
       if (e_prog + 8 * u < E) v = *(const u32x4*)(W1h + (size_t)d * E + e_prog + 8 * u);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const u16 x = (u16)(v[j >> 1] >> (16 * (j & 1)));
-        *(FMLP_LDS u16*)((FMLP_LDS char*)fmlp_lds + W1T_OFF + wt_off(8 * u + j, d >> 3) + (d & 7) * 2) = x;
+        *(FMLP_LDS u16*)((FMLP_LDS char*)fmlp_lds + W1T_OFF + wt_off<ET>(8 * u + j, d >> 3) + (d & 7) * 2) = x;
       }
     }
   }
@@ -475,8 +487,8 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
   auto issue_pair = [&](int i, int slot) {
 #pragma unroll
     for (int k = 0; k < NPL; ++k) {
-      const int region = (k * DW2_NT + wave * 64) / (SUB / 16);  // wave-uniform: 0 X0, 1 dO0, 2 X1, 3 dO1
-      const int r0 = b_lo + (2 * i + (region >> 1)) * DW_BT;
+      const int region = (k * DW2_NT + wave * 64) / (SUB / 16);  // wave-uniform: 2 s X of set s, 2 s + 1 dO
+      const int r0 = b_lo + (RS * i + (region >> 1)) * DW_BT;
       const int bytes = clamp0(b_hi - r0, DW_BT) * D * 2;
       const i32x4 rs = make_rsrc_words(((region & 1) ? dOh : Xh) + (size_t)r0 * D, bytes);
       buf_load16_lds(rs, pieceOff[k], RING_OFF + slot * PAIR + 16 * (k * DW2_NT + wave * 64));
@@ -492,7 +504,7 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
   //   B operand of Z / dH: weight-tile row 32 cg + l32, piece 2 ks + g -> offWt[ks % 2] + (ks / 2) * 8192
   int offWt[2];
 #pragma unroll
-  for (int kp = 0; kp < 2; ++kp) offWt[kp] = W1T_OFF + (int)wt_off(32 * cg + l32, 2 * kp + g);
+  for (int kp = 0; kp < 2; ++kp) offWt[kp] = W1T_OFF + (int)wt_off<ET>(32 * cg + l32, 2 * kp + g);
   //   B operand of dW2 / dW1^T (transposed subtile reads) -> offTr[r] + nt * 2048 + s * 1024
   int offTr[2];
 #pragma unroll
@@ -520,7 +532,7 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
       const int ks = q >> 1, which = q & 1;  // which 0 -> Z (X, W1T), 1 -> dH (dO, W2T)
       Opnd o;
       o.a = lds_read16(base + (which ? SUB : 0) + offRow[ks & 1] + (ks >> 1) * 2048);
-      o.b = lds_read16((which ? WT : 0) + offWt[ks & 1] + (ks >> 1) * 8192);
+      o.b = lds_read16((which ? WT : 0) + offWt[ks & 1] + (ks >> 1) * WTB);
       return o;
     };
     Opnd ring[PD + 1];
@@ -542,7 +554,7 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
   // first; the 8 K-step-0 MFMAs then run with elements 8-15 spread between them, and the
   // 8 K-step-1 MFMAs follow.
   // per-head dZ resource (DZ): Bp / 256 tiles of [nE * 128 rows e][256 positions]
-  const int Ep = nE * DW_ET;
+  const int Ep = nE * ET;
   const u16* dzh = DZ ? dzt + (size_t)h * Ep * Bp : nullptr;
   // lane part of the dZ store offsets inside a subtile's 2 KB block [32 columns][32 positions]
   unsigned dzLane[2];
@@ -632,9 +644,9 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
     };
     issue_pair(1, next);
     g1_phase(cur);
-    // first row of the subtile set `set` takes in pair i
-    auto row0 = [&](int i) { return b_lo + (2 * i + set) * DW_BT; };
-    if (set == 0) {
+    // first row of the subtile set `set` takes in group i
+    auto row0 = [&](int i) { return b_lo + (RS * i + set) * DW_BT; };
+    if (set < RS / 2) {
       ag2_phase(cur, row0(0));
       pair_end(AG);
       for (int i = 1; i < npair; ++i) {
@@ -659,12 +671,13 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
     wait_vmcnt<0>();
   }
 
-  // ---- add the two sets' partial sums through LDS (set 1 writes, set 0 adds) ----
+  // ---- add the sets' partial sums through LDS (sets 1 .. RS-1 write, set 0 adds them in order) ----
   asm volatile("" ::: "memory");
   __syncthreads();
   {
-    const int xb = cg * (2 * NTN * 16 * 256);  // 2 NTN accumulators x 16 registers x 64 lanes x 4 bytes
-    if (set == 1) {
+    constexpr int ACCB = 2 * NTN * 16 * 256;  // 2 NTN accumulators x 16 registers x 64 lanes x 4 bytes
+    const int xb = ((set > 0 ? set - 1 : 0) * CG + cg) * ACCB;
+    if (set > 0) {
 #pragma unroll
       for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
@@ -678,17 +691,21 @@ __device__ __forceinline__ void dw2_body(const u16* __restrict__ X, const u16* _
     __syncthreads();
     if (set == 0) {
 #pragma unroll
-      for (int nt = 0; nt < NTN; ++nt)
+      for (int so = 1; so < RS; ++so) {
+        const int sb = ((so - 1) * CG + cg) * ACCB;
 #pragma unroll
-        for (int i4 = 0; i4 < 4; ++i4) {
-          const u32x4 v2 = lds_read16(xb + ((nt * 4 + i4) * 64 + lane) * 16);
-          const u32x4 v1 = lds_read16(xb + (((NTN + nt) * 4 + i4) * 64 + lane) * 16);
+        for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            a2[nt][4 * i4 + j] += __uint_as_float(v2[j]);
-            a1[nt][4 * i4 + j] += __uint_as_float(v1[j]);
+          for (int i4 = 0; i4 < 4; ++i4) {
+            const u32x4 v2 = lds_read16(sb + ((nt * 4 + i4) * 64 + lane) * 16);
+            const u32x4 v1 = lds_read16(sb + (((NTN + nt) * 4 + i4) * 64 + lane) * 16);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              a2[nt][4 * i4 + j] += __uint_as_float(v2[j]);
+              a1[nt][4 * i4 + j] += __uint_as_float(v1[j]);
+            }
           }
-        }
+      }
       dw_store<BF16, D>(a1, a2, dW1, dW2, ws, H, E, h, s, nS, e0, g, l32, outf32);
     }
   }
@@ -703,12 +720,12 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
                               (E + 31) >> 5, nullptr);
 }
 
-template <bool BF16, int D, int ACT, bool HILO, bool DZ>
+template <bool BF16, int D, int ACT, bool HILO, bool DZ, int ET = DW_ET>
 __global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
            int H, int B, int E, int nE, int nS, int rows_per_split, int outf32, u16* __restrict__ dzt, int Bp) {
-  dw2_body<BF16, D, ACT, HILO, DZ>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32,
+  dw2_body<BF16, D, ACT, HILO, DZ, ET>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32,
                                    xcd_remap(blockIdx.x, gridDim.x), dzt, Bp);
 }
 
@@ -718,7 +735,7 @@ dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
 // use 8 waves (two per SIMD); the dynamic LDS is the dW role's (the larger). Each role's
 // tiles are remapped onto XCDs within its own range (exact when its count is a multiple of 8).
 static_assert(DW2_NT == DX2_NT, "both roles run with the same workgroup size");
-template <bool BF16, int D, int ACT, bool HILO, int DES>
+template <bool BF16, int D, int ACT, bool HILO, int DES, int ET = DW_ET>
 __global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            const u16* __restrict__ dO, void* __restrict__ dX, void* __restrict__ dW1, void* __restrict__ dW2,
@@ -738,7 +755,8 @@ bwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   }
   const int bw = dx_first ? b - n_dx : b;  // index among the dW programs (< 0 or >= n_dw: a dX program)
   if (bw >= 0 && bw < n_dw) {
-    dw2_body<BF16, D, ACT, HILO>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32, xcd_remap(bw, n_dw));
+    dw2_body<BF16, D, ACT, HILO, false, ET>(X, W1, W2, dO, dW1, dW2, ws, H, B, E, nE, nS, rows_per_split, outf32,
+                                            xcd_remap(bw, n_dw));
   } else {
     const int bx = dx_first ? b : b - n_dw;
     const int m = xcd_remap(bx, n_dx);
@@ -1067,8 +1085,13 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
     }
   }
   BwdPlan p{};
-  p.nE = (int)((E + DW_ET - 1) / DW_ET);
-  const long long base = H * (long long)p.nE, N = num_cus > 0 ? num_cus : 1;
+  const long long N = num_cus > 0 ? num_cus : 1;
+  // dW programs of ET E-columns: 128, or at D = 64 with the dX programs' E split also 64 (twice
+  // the programs, each half the work, for grids that leave CUs idle); FMLP_BWD_ET (read once per
+  // process) forces 128 or 64 where allowed
+  static const int et_env = env_int("FMLP_BWD_ET", 0);
+  auto nE_for = [&](long long et) { return (E + et - 1) / et; };
+  const long long base = H * nE_for(DW_ET);  // the stored-dZ form's dW programs (128 columns)
   auto ws_for = [&](long long ns) { return ns > 1 ? (size_t)2 * ns * H * E * D * sizeof(float) : (size_t)0; };
   // dX programs of 256 rows, or at D = 64 of 128 rows with E in two parts (half the time each)
   auto n_dx_for = [&](int des) { return H * ((B + DX2_ROWS / des - 1) / (DX2_ROWS / des)); };
@@ -1076,13 +1099,20 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
     return kPlanFixedUs + (double)(DX2_ROWS / des) * E * (3.0 * D + valu_dx(act) * kPlanValuMacs) / kPlanRate;
   };
   const int max_des = D == 64 ? 2 : 1;
-  const double w_per_row = 128.0 * ((hilo ? 6.0 : 4.0) * D + valu_dw(act) * kPlanValuMacs) / kPlanRate;
+  auto w_per_row_for = [&](long long et) {
+    return (double)et * ((hilo ? 6.0 : 4.0) * D + valu_dw(act) * kPlanValuMacs) / kPlanRate;
+  };
+  const double w_per_row = w_per_row_for(DW_ET);
   // candidates nS = 1, 2, 4, ... up to B / 256 and two dW programs per CU (which keeps the fp32
   // partials within 64 MiB at D <= 128 on 256 CUs), whose workspace fits max_ws
   const long long max_ns = B / 256 > 1 ? B / 256 : 1;
-  long long cap = base > 0 ? 2 * N / base : 1;
-  if (cap < 1) cap = 1;
-  if (cap > max_ns) cap = max_ns;
+  auto cap_for = [&](long long nprog) {
+    long long c = nprog > 0 ? 2 * N / nprog : 1;
+    if (c < 1) c = 1;
+    if (c > max_ns) c = max_ns;
+    return c;
+  };
+  const long long cap = cap_for(base);
   // FMLP_BWD_NS / FMLP_BWD_ORDER (read once per process) force the split and the order
   // (1: dW programs first, 2: dX programs first)
   static const int ns_env = env_int("FMLP_BWD_NS", 0);
@@ -1102,42 +1132,50 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
   double best_t = 0.0;
   long long best_ns = 1;
   bool best_dx_first = false, best_dxs = false;
-  int best_des = 1;
+  int best_des = 1, best_et = DW_ET;
   for (int des = 1; des <= max_des; ++des) {
     if (des_env > 0 && des != des_env) continue;
     if (fixed_des > 0 && des != fixed_des) continue;
     const long long n_dx = n_dx_for(des), T_dx = n_dx / (H > 0 ? H : 1);
     const double tx = tx_for(des);
     const bool rag = B % (DX2_ROWS / des) != 0 && T_dx >= 2 && dxs_xs >= 2 && dxs_env != 0 && fixed_dxs != 0;
-    for (long long ns = 1; ns <= (ns_env > 0 ? 1 : cap); ns *= 2) {
-      const long long want = ns_env > 0 ? (ns_env < max_ns ? ns_env : max_ns) : ns;
-      const long long rps = rows_for_split(B, want), eff = B > rps ? (B + rps - 1) / rps : 1;
-      if (eff > 1 && ws_for(eff) > max_ws) break;
-      const double tw = kPlanFixedUs + (double)rps * w_per_row;
-      const long long n_dw = base * eff;
-      const double red = eff > 1 ? kPlanLaunchUs + (double)(2 * eff + 1) * H * E * D * 4.0 / kPlanHbmBytesPerUs : 0.0;
-      const bool dxs_fits = rag && (ws_for(eff) + 255) / 256 * 256 + dxs_bytes(des) <= max_ws;
-      for (int split = 0; split <= 1; ++split) {
-        if (split ? !dxs_fits : fixed_dxs == 1 && dxs_fits) continue;
-        // the split tiles' work, spread over the device, and the launch that sums them
-        const long long nx = split ? n_dx - H : n_dx;
-        const double extra =
-            split ? (double)H * dxs_xs * (kPlanFixedUs + (tx - kPlanFixedUs) / dxs_xs) / N + kPlanLaunchUs : 0.0;
-        for (int o = 1; o <= 2; ++o) {
-          if (order_env && o != order_env) continue;
-          const double t =
-              (o == 1 ? list_makespan(n_dw, tw, nx, tx, N) : list_makespan(nx, tx, n_dw, tw, N)) + red + extra;
-          if (best_t == 0.0 || t < best_t) {
-            best_t = t;
-            best_ns = eff;
-            best_dx_first = o == 2;
-            best_des = des;
-            best_dxs = split == 1;
+    for (int et = DW_ET; et >= 64; et /= 2) {
+      if (et != DW_ET && !(D == 64 && des == 2)) continue;
+      if (et_env > 0 && et != et_env && (et_env == DW_ET || (D == 64 && des == 2))) continue;
+      const long long base_et = H * nE_for(et), cap_et = cap_for(base_et);
+      const double wrow = w_per_row_for(et);
+      for (long long ns = 1; ns <= (ns_env > 0 ? 1 : cap_et); ns *= 2) {
+        const long long want = ns_env > 0 ? (ns_env < max_ns ? ns_env : max_ns) : ns;
+        const long long rps = rows_for_split(B, want), eff = B > rps ? (B + rps - 1) / rps : 1;
+        if (eff > 1 && ws_for(eff) > max_ws) break;
+        const double tw = kPlanFixedUs + (double)rps * wrow;
+        const long long n_dw = base_et * eff;
+        const double red = eff > 1 ? kPlanLaunchUs + (double)(2 * eff + 1) * H * E * D * 4.0 / kPlanHbmBytesPerUs : 0.0;
+        const bool dxs_fits = rag && (ws_for(eff) + 255) / 256 * 256 + dxs_bytes(des) <= max_ws;
+        for (int split = 0; split <= 1; ++split) {
+          if (split ? !dxs_fits : fixed_dxs == 1 && dxs_fits) continue;
+          // the split tiles' work, spread over the device, and the launch that sums them
+          const long long nx = split ? n_dx - H : n_dx;
+          const double extra =
+              split ? (double)H * dxs_xs * (kPlanFixedUs + (tx - kPlanFixedUs) / dxs_xs) / N + kPlanLaunchUs : 0.0;
+          for (int o = 1; o <= 2; ++o) {
+            if (order_env && o != order_env) continue;
+            const double t =
+                (o == 1 ? list_makespan(n_dw, tw, nx, tx, N) : list_makespan(nx, tx, n_dw, tw, N)) + red + extra;
+            if (best_t == 0.0 || t < best_t) {
+              best_t = t;
+              best_ns = eff;
+              best_dx_first = o == 2;
+              best_des = des;
+              best_dxs = split == 1;
+              best_et = et;
+            }
           }
         }
       }
     }
   }
+  p.et_w = best_et;
   p.dx_es = best_des;
   p.dx_tiles_per_head = (int)((B + DX2_ROWS / best_des - 1) / (DX2_ROWS / best_des));
   p.n_dx = (long long)p.dx_tiles_per_head * H;
@@ -1154,7 +1192,7 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
   static const int dz_env = env_int("FMLP_BWD_DZ", -1);
   const int dz_want = dz_mode != DZ_AUTO ? (dz_mode == DZ_FORCE ? 1 : 0) : dz_env;
   const long long Bp = (B + DX2_ROWS - 1) / DX2_ROWS * DX2_ROWS;
-  const size_t dz_head = (size_t)p.nE * DW_ET * (size_t)Bp * 2u;
+  const size_t dz_head = (size_t)nE_for(DW_ET) * DW_ET * (size_t)Bp * 2u;
   double best_dz = 0.0;
   long long best_dz_ns = 1;
   if (dz_want != 0 && B > 0 && dz_head < ((size_t)1 << 31)) {
@@ -1181,11 +1219,13 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
     p.dx_tiles_per_head = (int)((B + DX2_ROWS - 1) / DX2_ROWS);
     p.dxs_xs = 0;
     p.dxs_nct = 0;
+    p.et_w = DW_ET;
   }
+  p.nE = (int)nE_for(p.et_w);
   const long long rps = rows_for_split(B, best_ns);
   p.nS = (int)(B > rps ? (B + rps - 1) / rps : 1);
   p.rows_per_split = (int)rps;
-  p.n_dw = base * p.nS;
+  p.n_dw = H * (long long)p.nE * p.nS;
   p.dx_first = best_dx_first;
   p.ws_bytes = ws_for(p.nS);
   if (p.dxs_xs > 0) {  // the split dX tiles' partials after the dW partials
@@ -1236,14 +1276,21 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo,
   return p;
 }
 
-template <bool BF16, int D, int ACT, int DES>
+// dynamic LDS of the dW role: a 3-group ring of subtiles and the two weight tiles
+template <int D, int ET>
+constexpr size_t dw_lds_bytes() {
+  return 3u * 2u * (DW2_NW / (ET / 32)) * 64u * D + 2u * 2u * ET * D;
+}
+
+template <bool BF16, int D, int ACT, int DES, int ET>
 static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
   if (p.n_dw + p.n_dx + p.n_dxs > 0x7fffffffLL || (long long)p.dx_tiles_per_head * a.H > 0x7fffffffLL)
     return hipErrorInvalidValue;
   hipError_t e;
   // the dW role's: two weight tiles and three subtile pairs (256 D bytes each); at least the
   // dX role's rings (one or two parts of DX_NSLOT slots of 128 D bytes)
-  constexpr size_t lds = std::max<size_t>(1280u * D, (size_t)DES * DX_NSLOT * 128u * D);
+  constexpr size_t lds = std::max<size_t>(dw_lds_bytes<D, ET>(), (size_t)DES * DX_NSLOT * 128u * D);
+  static_assert(dw_lds_bytes<D, DW_ET>() == 1280u * D, "the 128-column form's LDS");
   auto reduce = [&]() {          // sum of the dW programs' fp32 partials when B is split
     if (p.nS <= 1) return hipSuccess;
     const size_t items = 2 * ((size_t)a.H * a.E * a.D / 4);
@@ -1293,7 +1340,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
                          p.dxs_nct, dxs_ws);
       return hipGetLastError();
     };
-    e = a.dw_hilo ? launch_u(bwd_kernel<BF16, D, ACT, true, DES>) : launch_u(bwd_kernel<BF16, D, ACT, false, DES>);
+    e = a.dw_hilo ? launch_u(bwd_kernel<BF16, D, ACT, true, DES, ET>) : launch_u(bwd_kernel<BF16, D, ACT, false, DES, ET>);
     if (e != hipSuccess) return e;
     if ((e = reduce()) != hipSuccess || p.n_dxs == 0) return e;
     // the ragged dX tiles' partials: split tile s is head s's last tile
@@ -1310,7 +1357,8 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
                          (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, a.out_f32 ? 1 : 0, (u16*)nullptr, 0);
       return hipGetLastError();
     };
-    e = a.dw_hilo ? launch_w(dw2_kernel<BF16, D, ACT, true, false>) : launch_w(dw2_kernel<BF16, D, ACT, false, false>);
+    e = a.dw_hilo ? launch_w(dw2_kernel<BF16, D, ACT, true, false, ET>)
+                  : launch_w(dw2_kernel<BF16, D, ACT, false, false, ET>);
     if (e != hipSuccess) return e;
     if ((e = reduce()) != hipSuccess) return e;
   }
@@ -1332,9 +1380,10 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
 template <bool BF16, int D, int ACT>
 static hipError_t launch_bwd_e(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {
   if constexpr (D == 64) {
-    if (p.dx_es == 2) return launch_bwd_t<BF16, D, ACT, 2>(a, p, st);
+    if (p.dx_es == 2 && p.et_w == 64) return launch_bwd_t<BF16, D, ACT, 2, 64>(a, p, st);
+    if (p.dx_es == 2) return launch_bwd_t<BF16, D, ACT, 2, DW_ET>(a, p, st);
   }
-  return launch_bwd_t<BF16, D, ACT, 1>(a, p, st);
+  return launch_bwd_t<BF16, D, ACT, 1, DW_ET>(a, p, st);
 }
 
 template <bool BF16, int D>

@@ -50,7 +50,8 @@ FwdPlan fwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t
 //   Stored-dZ form (dz): the dW programs also store dZ to the workspace and dX is a GEMM over
 //   it (dxg_kernel), two launches instead of recomputing Z and dH in dX programs.
 struct BwdPlan {
-  int nE;              // E-tiles of 128 per head
+  int et_w;            // E-columns per dW program: 128, or 64 (D = 64, with dx_es == 2)
+  int nE;              // E-tiles of et_w per head
   int nS;              // B splits for the dW programs
   int rows_per_split;  // multiple of 32
   int dx_tiles_per_head;

@@ -160,10 +160,11 @@ size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int 
 int fmlp_bwd_stores_dz(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act);
 
 /* The tuned backward's plan for these shapes, dtype flags and activation on the current
- * device, written to info[0 .. n_info - 1] (at most 10 values, in this order): stored-dZ form
+ * device, written to info[0 .. n_info - 1] (at most 11 values, in this order): stored-dZ form
  * (0/1), B splits of the dW programs, dX programs' in-workgroup E parts, parts of each split
  * ragged dX tile (0: not split), dX programs first (0/1), dW programs, whole-tile dX programs,
- * split-tile dX programs, workspace bytes, and the activation's code. Returns FMLP_OK, or
+ * split-tile dX programs, workspace bytes, the activation's code, and the E-columns per dW
+ * program (128 or 64). Returns FMLP_OK, or
  * FMLP_ERR_UNSUPPORTED for shapes the tuned kernels do not take. No counterpart in the
  * reference: a diagnostic for tests and benches. */
 int fmlp_bwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, int64_t* info, int n_info);
