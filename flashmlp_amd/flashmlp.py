@@ -165,7 +165,8 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
     if _fast is not None:  # 16-bit, one GPU, dense and aligned, a tuned shape: else None
         r = _fast.fwd(x, w1, w2, _act_code(activation))
         if r is not None:
-            _lib.check(r[0], "forward")
+            if r[0]:
+                _lib.check(r[0], "forward")
             return r[1]
     dtype = _io_code(x, w1, w2)
     o = _empty_as(x, (H, B, D))
@@ -228,7 +229,8 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
     if _fast is not None and (need_dx or need_dw):  # as in flashmlp_fwd
         r = _fast.bwd(x, w1, w2, do, _act_code(activation), flags)
         if r is not None:
-            _lib.check(r[0], "backward")
+            if r[0]:
+                _lib.check(r[0], "backward")
             return r[1], r[2], r[3]
     dtype = _io_code(x, w1, w2, do)
     flags |= dtype
