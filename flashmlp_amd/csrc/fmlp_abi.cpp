@@ -94,6 +94,10 @@ size_t elem_bytes(int io) { return io == FMLP_DTYPE_F32 ? 4 : 2; }
 bool tuned_shape(int64_t D, int64_t E, int io) {
   return (io == FMLP_DTYPE_F16 || io == FMLP_DTYPE_BF16) && (D == 64 || D == 128) && E % 8 == 0;
 }
+// the tuned forward also takes D = 256 (one wave per SIMD); the backward runs it generically
+bool fwd_tuned_shape(int64_t D, int64_t E, int io) {
+  return tuned_shape(D, E, io) || ((io == FMLP_DTYPE_F16 || io == FMLP_DTYPE_BF16) && D == 256 && E % 8 == 0);
+}
 
 int check_shape(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   if (H < 0 || B < 0 || D < 0 || E < 0)
@@ -248,7 +252,7 @@ int fwd_impl(const void* x, const void* w1, const void* w2, void* o, int64_t H, 
   if (!rows) return ok();
   const bool dense = sx == nullptr || (is_dense3(sx, B, D) && is_dense3(sw1, D, E) && is_dense3(sw2, E, D));
   hipError_t e;
-  if (dense && tuned_shape(D, E, io) && aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(o)) {
+  if (dense && fwd_tuned_shape(D, E, io) && aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(o)) {
     int cus = 0;
     if ((st = num_cus_current(&cus))) return st;
     fmlp::FwdArgs a{x, w1, w2, o, H, B, D, E, io == FMLP_DTYPE_BF16, act, (dtype & FMLP_OUT_F32) != 0, cus};
@@ -280,7 +284,7 @@ FMLP_EXPORT int fmlp_fwd(const void* x, const void* w1, const void* w2, void* o,
 }
 
 FMLP_EXPORT size_t fmlp_fwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
-  if (check_shape(H, B, D, E, dtype) != FMLP_OK || !tuned_shape(D, E, io_of(dtype))) return 0;
+  if (check_shape(H, B, D, E, dtype) != FMLP_OK || !fwd_tuned_shape(D, E, io_of(dtype))) return 0;
   int cus = 0;
   if (num_cus_current(&cus) != FMLP_OK) return 0;
   return fmlp::fwd_plan(H, B, D, E, cus, (size_t)-1).ws_bytes;

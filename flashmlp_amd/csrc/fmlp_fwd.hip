@@ -57,13 +57,20 @@ __device__ __forceinline__ TileId main_tile(int m, int n_split, int H, int T) {
   const int m2 = m - first, tb = T - a - 1;
   return TileId{H - b + m2 / tb, m2 % tb};
 }
-__host__ __device__ constexpr int fwd_waves(int D) { return D / 16; }
-constexpr int FWD_NSLOT = 8;  // LDS ring slots (chunks)
-constexpr int FWD_PF = 4;     // chunks loaded ahead (with one barrier per chunk)
-constexpr int FWD_SB = 2;     // chunk iterations per workgroup barrier
+// Waves per workgroup: D / 16 up to D = 128 (two waves per SIMD, the threads covering a chunk's
+// 4 D pieces of W1c and of W2c once); 4 at D = 256 (one wave per SIMD, whose O accumulators alone
+// take 128 registers; each thread loads 4 pieces per region).
+__host__ __device__ constexpr int fwd_waves(int D) { return D <= 128 ? D / 16 : 4; }
+__host__ __device__ constexpr int fwd_wpe(int D) { return D <= 128 ? 2 : 1; }  // waves per SIMD
+// ring geometry: slots (chunks of 128 D bytes), chunk iterations per workgroup barrier and chunks
+// loaded ahead; at D = 256 a chunk is 32 KB, so four slots, a barrier per chunk, two ahead
+constexpr int FWD_PF = 4;  // chunks loaded ahead with one barrier per chunk (D <= 128)
+__host__ __device__ constexpr int fwd_nslot(int D) { return D <= 128 ? 8 : 4; }
+__host__ __device__ constexpr int fwd_sb(int D) { return D <= 128 ? 2 : 1; }
+__host__ __device__ constexpr int fwd_pf(int D) { return D <= 128 ? FWD_PF + fwd_sb(D) - 1 : 2; }
 
 template <bool BF16, int D, int ACT, int ES>
-__global__ void __launch_bounds__(fwd_waves(D) * ES * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
+__global__ void __launch_bounds__(fwd_waves(D) * ES * 64) __attribute__((amdgpu_waves_per_eu(fwd_wpe(D), fwd_wpe(D))))
 fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            void* __restrict__ O, int B, int E, int H, int tiles_per_head, int outf32, int n_main, int n_split,
            int xs, int nct, float* __restrict__ ws) {
@@ -77,8 +84,9 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   // SB: chunk iterations per workgroup barrier. The loads run SB - 1 chunks further ahead so
   // that a barrier covers the SB chunks read after it (measured on MI355X at cfg4: SB = 2 is
   // about 1 % faster than a barrier per chunk).
-  constexpr int SB = FWD_SB;
-  constexpr int NSLOT = FWD_NSLOT, PF = FWD_PF + (SB - 1);
+  constexpr int SB = fwd_sb(D);
+  constexpr int NSLOT = fwd_nslot(D), PF = fwd_pf(D);
+  constexpr int NPR = 4 * D / NT;  // 16-byte pieces per thread per region (W1c or W2c) of a chunk
   static_assert(SB == 1 || SB == 2, "barrier spacing");
   static_assert(PF >= 2 && PF <= NSLOT - 2 - (SB - 1) && (NSLOT & (NSLOT - 1)) == 0, "ring");
 
@@ -109,7 +117,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const int NC = (ce - cb + ES - 1) / ES;
   const int c0 = cb + part * NC;
   const int e_end = min(E, ce * 32);  // columns of W1 (rows of W2) this workgroup reads
-  const unsigned RB = (unsigned)part * FWD_NSLOT * 128u * D;  // this part's ring
+  const unsigned RB = (unsigned)part * NSLOT * 128u * D;  // this part's ring
 
   const u16* Xh = X + (size_t)h * B * D;
   const u16* W1h = W1 + (size_t)h * D * E;
@@ -117,14 +125,20 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   const int b_wave = bt * BB + wave * 32;
 
   // ---- chunk staging: buffer-to-LDS loads, PF chunks ahead into an NSLOT-slot ring ----
-  // One 16-byte piece per thread per region (NT == 4 D): piece p = tid of W1c lands at slot
-  // offset 16 p (row d = p / 4, columns 8 (p % 4) ..), piece p of W2c at W2OFF + 16 p (block
-  // p / 128, row (p / 4) % 32, columns 32 (p / 128) + 8 (p % 4) ..). Columns past E (and every
-  // piece of a chunk past the last) are out of range and land as zeros.
-  static_assert(NT == 4 * D, "one piece per thread per region");
-  const int colq = (tid & 3) * 8;
-  const unsigned dOffW1 = (unsigned)(tid >> 2) * (unsigned)E * 2u + (tid & 3u) * 16u;
-  const unsigned dOffW2 = ((tid >> 2) & 31u) * (D * 2u) + (unsigned)(tid >> 7) * 64u + (tid & 3u) * 16u;
+  // NPR 16-byte pieces per thread per region: piece p = tid + k NT of W1c lands at slot offset
+  // 16 p (row d = p / 4, columns 8 (p % 4) ..), piece p of W2c at W2OFF + 16 p (block p / 128,
+  // row (p / 4) % 32, columns 32 (p / 128) + 8 (p % 4) ..). Columns past E (and every piece of a
+  // chunk past the last) are out of range and land as zeros.
+  static_assert(NPR * NT == 4 * D, "the threads cover a region's pieces");
+  int colq[NPR];
+  unsigned dOffW1[NPR], dOffW2[NPR];
+#pragma unroll
+  for (int k = 0; k < NPR; ++k) {
+    const unsigned p = (unsigned)(tid + k * NT);
+    colq[k] = (int)(p & 3u) * 8;
+    dOffW1[k] = (p >> 2) * (unsigned)E * 2u + (p & 3u) * 16u;
+    dOffW2[k] = ((p >> 2) & 31u) * (D * 2u) + (p >> 7) * 64u + (p & 3u) * 16u;
+  }
   auto dma_chunk = [&](int c) {
     const int cg = c0 + c;
     const int lim = e_end - cg * 32;
@@ -132,13 +146,16 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     const i32x4 r1 = make_rsrc_words(W1h + (size_t)cg * 32, rem > 0 ? rem : 0);
     const i32x4 r2 = make_rsrc_words(W2h + (size_t)cg * 32 * D, clamp0(lim, 32) * D * 2);
     const int slot = (int)RB + (c & (NSLOT - 1)) * (int)SLOT + wave * 1024;
-    buf_load16_lds(r1, colq < lim ? dOffW1 : BUF_OOB, slot);
-    buf_load16_lds(r2, dOffW2, slot + (int)W2OFF);
+#pragma unroll
+    for (int k = 0; k < NPR; ++k) {
+      buf_load16_lds(r1, colq[k] < lim ? dOffW1[k] : BUF_OOB, slot + k * NT * 16);
+      buf_load16_lds(r2, dOffW2[k], slot + (int)W2OFF + k * NT * 16);
+    }
   };
   // end of a chunk: the LDS stores are retired and visible after the barrier; the loads of
   // the chunk after next stay in flight (their data is waited for where it is stored)
   auto chunk_end = [&]() {
-    wait_vmcnt<2 * (PF - 1 - SB)>();     // this wave's pieces of the SB chunks read next
+    wait_vmcnt<2 * NPR * (PF - 1 - SB)>();  // this wave's pieces of the SB chunks read next
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -178,7 +195,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   // ---- prologue: chunks 0 .. PF-1 requested, chunk 0 waited for, Z^T(0) ----
 #pragma unroll
   for (int c = 0; c < PF; ++c) dma_chunk(c);
-  wait_vmcnt<2 * (PF - 2)>();  // chunks 0 and 1
+  wait_vmcnt<2 * NPR * (PF - 2)>();  // chunks 0 and 1
   __builtin_amdgcn_s_waitcnt(0xC07F);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
@@ -203,7 +220,8 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     constexpr bool DO_G1 = decltype(G1)::value;
     constexpr bool DO_G2 = decltype(G2)::value;
     constexpr int N1 = DO_G1 ? KS : 0, N2 = DO_G2 ? KS : 0, NOPS = N1 + N2;
-    constexpr int PER = 16 / NOPS;  // activation elements per step
+    // activation elements of step j: [16 j / NOPS, 16 (j + 1) / NOPS) (one or two per step at
+    // D <= 128, one every other step at D = 256)
     const unsigned base1 = RB + ((c + 1) & (NSLOT - 1)) * SLOT, base2 = RB + ((c - 1) & (NSLOT - 1)) * SLOT;
 
     // chunk c+PF is requested straight into its LDS slot (PF chunks ahead of the one read)
@@ -234,8 +252,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
         o[nt] = mfma<BF16>(s == 0 ? in.h0 : in.h1, cur, o[nt]);
       }
 #pragma unroll
-      for (int q = 0; q < PER; ++q) {
-        const int e = j * PER + q;
+      for (int e = 16 * j / NOPS; e < 16 * (j + 1) / NOPS; ++e) {
         hv[e] = act_f<ACT>(in.z[e]);
         if (e & 1) {
           const unsigned pk = pack2<BF16>(hv[e - 1], hv[e]);
@@ -378,7 +395,7 @@ fwd_reduce_kernel(const float* __restrict__ ws, void* __restrict__ O, int B, int
 // FMLP_FWD_XS=0 (read once per process) turns the cross-workgroup split off.
 FwdPlan fwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t max_ws) {
   FwdPlan p{};
-  const long long BB = 2 * D, T = (B + BB - 1) / BB, R = H * T, N = num_cus > 0 ? num_cus : 1;
+  const long long BB = 32 * fwd_waves((int)D), T = (B + BB - 1) / BB, R = H * T, N = num_cus > 0 ? num_cus : 1;
   const long long nch = (E + 31) / 32;
   // in-workgroup split at D = 64 when the tiles fit on the CUs at one workgroup each (the
   // unsplit kernel would leave a SIMD with one wave) and each part gets at least two chunks;
@@ -420,7 +437,7 @@ FwdPlan fwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t
 
 template <bool BF16, int D, int ACT, int ES>
 static hipError_t launch_fwd_e(const FwdArgs& a, const FwdPlan& p, int tiles_per_head, hipStream_t st) {
-  const size_t lds = (size_t)ES * FWD_NSLOT * 128u * D;
+  const size_t lds = (size_t)ES * fwd_nslot(D) * 128u * D;
   auto k = fwd_kernel<BF16, D, ACT, ES>;
   static std::atomic<unsigned long long> lds_set{0};
   hipError_t e = set_lds_once((const void*)k, (int)lds, lds_set);
@@ -475,9 +492,11 @@ static hipError_t launch_fwd_a(const FwdArgs& a, hipStream_t st) {
 
 hipError_t launch_fwd(const FwdArgs& a, hipStream_t st) {
   if (a.bf16) {
+    if (a.D == 256) return launch_fwd_a<true, 256>(a, st);
     if (a.D == 128) return launch_fwd_a<true, 128>(a, st);
     return launch_fwd_a<true, 64>(a, st);
   }
+  if (a.D == 256) return launch_fwd_a<false, 256>(a, st);
   if (a.D == 128) return launch_fwd_a<false, 128>(a, st);
   return launch_fwd_a<false, 64>(a, st);
 }

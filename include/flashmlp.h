@@ -111,7 +111,9 @@ int fmlp_shape_supported(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
 /* 1 when the tuned kernels take these shapes (16-bit io, D in {64, 128}, E % 8 == 0) on dense,
  * 16-byte aligned tensors; other supported shapes, dtypes and layouts run on the generic
- * kernels. No counterpart in the reference (its Triton kernels are autotuned per shape). */
+ * kernels, except that the tuned forward also takes D = 256 (16-bit io, E % 8 == 0, dense,
+ * aligned; its backward is generic). No counterpart in the reference (its Triton kernels are
+ * autotuned per shape). */
 int fmlp_shape_tuned(int64_t D, int64_t E, int dtype);
 
 /*

@@ -107,7 +107,9 @@ def test_fp32_cfg1_shape():
 
 @pytest.mark.parametrize("D,dt", [(32, torch.bfloat16), (256, torch.float16), (64, torch.float32)])
 def test_strided_views_are_read_in_place(D, dt):
-    H, B, E = 3, 70, 40
+    # both calls on the generic kernels: at D = 256 an E that is no multiple of 8 keeps the dense
+    # forward off the tuned kernel (which takes dense D = 256 inputs with E % 8 == 0)
+    H, B, E = 3, 70, (44 if D == 256 else 40)
     x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=8))
     o_ref = fm.flashmlp_fwd(x, w1, w2, "silu")
     g_ref = fm.flashmlp_bwd(x, w1, w2, do, "silu")
