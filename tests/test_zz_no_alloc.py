@@ -63,8 +63,11 @@ def _bwd_noalloc(L, x, w1, w2, do, act, flags=0):
 def test_noalloc_matches_workspace_entry_point_twice():
     L = _lib.lib()
     # first: the cfg3 shape in the recompute-only form (B split, 16.8 MB or more of partials);
-    # second: smaller, whatever form the plan picks (its workspace fits the scratch either way)
+    # then smaller ones, whatever form the plan picks (its workspace fits the scratch either
+    # way): cfg5, whose ragged dX tiles are split over E (fp32 partials in the scratch) next to
+    # 64-column dW programs, and a small tail shape
     cases = [(16, 8192, 128, 512, torch.bfloat16, "leaky_relu", 21, _lib.FMLP_BWD_RECOMPUTE),
+             (8, 4097, 64, 2048, torch.float16, "sigmoid", 24, 0),
              (6, 1500, 64, 264, torch.float16, "silu", 22, 0)]
     for H, B, D, E, dt, act, seed, flags in cases:
         _say(f"[noalloc] H={H} B={B} D={D} E={E} {dt} act='{act}' seed={seed} flags={flags:#x}")
