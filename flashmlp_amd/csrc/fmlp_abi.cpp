@@ -374,7 +374,7 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
                                        is_dense3(sdo, B, D));
   const bool aligned = aligned16(x) && aligned16(w1) && aligned16(w2) && aligned16(dout) && aligned16(dx) &&
                        aligned16(dw1) && aligned16(dw2);
-  hipError_t e;
+  hipError_t e = hipSuccess;
   if (dense && aligned && tuned_shape(D, E, io)) {
     int cus = 0;
     if ((st = num_cus_current(&cus))) return st;
@@ -435,7 +435,15 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
         g.ws = ws;
       }
     }
-    e = fmlp::launch_gen_bwd(g, (hipStream_t)stream);
+    // dense 16-bit D = 256 with E % 8 == 0: dX on the tuned dX programs, dW on the generic kernels
+    const bool dx256 = want_dx && dense && aligned && fwd_tuned_shape(D, E, io) && !tuned_shape(D, E, io);
+    if (dx256) {
+      fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io == FMLP_DTYPE_BF16, act, nullptr,
+                      (dtype & FMLP_OUT_F32) != 0, false, true, false};
+      e = fmlp::launch_dx256(a, (hipStream_t)stream);
+      g.want_dx = 0;
+    }
+    if (e == hipSuccess && (g.want_dx || g.want_dw)) e = fmlp::launch_gen_bwd(g, (hipStream_t)stream);
   }
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return ok();

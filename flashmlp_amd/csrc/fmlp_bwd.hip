@@ -124,6 +124,10 @@ constexpr int DX2_ROWS = DX2_NW * 32;
 constexpr int DX_NSLOT = 8;  // chunk ring slots (128 D bytes each)
 constexpr int DX_PF = 4;     // chunks requested ahead of the one read
 static_assert(DX_PF <= DX_NSLOT - 2, "a slot is reloaded only after the barrier that retires its last reader");
+// At D = 256 (dX only; the dW role's tiles do not fit the LDS there) a program is 4 waves of 32
+// rows at one wave per SIMD, and a chunk is 32 KB: a 4-slot ring two chunks ahead.
+__host__ __device__ constexpr int dx_nslot(int D) { return D <= 128 ? DX_NSLOT : 4; }
+__host__ __device__ constexpr int dx_pf(int D) { return D <= 128 ? DX_PF : 2; }
 
 // DES = 2 (E split, D = 64 only: grids of 256-row dX programs that leave CUs idle): a program
 // owns 128 rows; waves 0-3 walk the first half of the E-chunks and waves 4-7 the second, each
@@ -134,19 +138,23 @@ __host__ __device__ constexpr int dx2_rows() { return DX2_ROWS / DES; }
 
 // A program owns tile t's rows and the E-chunks [cb, ce); with pws set (a ragged tile split
 // over E) it stores its fp32 partial dX tile there ([rows][D]) instead of writing dX.
-template <bool BF16, int D, int ACT, int DES = 1>
+template <bool BF16, int D, int ACT, int DES = 1, int NW = DX2_NW>
 __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* __restrict__ W1,
                                          const u16* __restrict__ W2, const u16* __restrict__ dO,
                                          void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32,
                                          int t, int cb, int ce, float* __restrict__ pws) {
   static_assert(DES == 1 || (DES == 2 && D == 64), "E split");
+  static_assert(NW == DX2_NW || (NW == 4 && D == 256 && DES == 1), "waves per program");
   constexpr int KS = D / 16, NTN = D / 32;
   constexpr unsigned SLOT = 128u * D;
   constexpr unsigned W2OFF = 64u * D;
-  constexpr int NTP = DX2_NT / DES;      // threads of one E part
+  constexpr int NTP = NW * 64 / DES;     // threads of one E part
+  constexpr int ROWS = NW * 32 / DES;    // rows per program
   constexpr int NDMA = 8 * D / NTP;      // 16-byte pieces per lane per chunk
   constexpr int N1 = 2 * KS, N2 = 2 * NTN;
   constexpr int PD = 3;
+  constexpr int NSL = dx_nslot(D), PF = dx_pf(D);
+  static_assert(PF <= NSL - 2 && NDMA * NTP == 8 * D, "ring and pieces");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform for the compiler
@@ -159,14 +167,16 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
   const int NCP = (NC + DES - 1) / DES;             // chunks per part: global chunk c0 + ci
   const int c0 = cb + part * NCP;
   const int e_end = min(E, ce * 32);                // columns of W1 (rows of W2) read
-  const int RB = part * DX_NSLOT * (int)SLOT;       // this part's ring
-  const bool late = wave >= 4;  // VALU-first half of the workgroup (the second part when split)
+  const int RB = part * NSL * (int)SLOT;            // this part's ring
+  // VALU-first half of the workgroup (the second part when split); with one wave per SIMD
+  // (NW = 4) every wave runs the MFMA-first order
+  const bool late = NW == 8 && wave >= 4;
 
   const u16* Xh = X + (size_t)h * B * D;
   const u16* dOh = dO + (size_t)h * B * D;
   const u16* W1h = W1 + (size_t)h * D * E;
   const u16* W2h = W2 + (size_t)h * E * D;
-  const int b_wave = bt * dx2_rows<D, DES>() + wp * 32;
+  const int b_wave = bt * ROWS + wp * 32;
 
   // ---- staging pieces: piece p (16 bytes at slot offset 16 p) of a chunk ----
   unsigned dmaOff[NDMA];
@@ -185,7 +195,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
       dmaCol[k] = -1;
     }
   }
-  // chunk staging: buffer-to-LDS loads DX_PF chunks ahead into a DX_NSLOT-slot ring; part chunk
+  // chunk staging: buffer-to-LDS loads PF chunks ahead into an NSL-slot ring; part chunk
   // ci is global chunk c0 + ci, and chunks past the part's share (or past the range) load as zeros
   auto dma_chunk = [&](int ci) {
     const int c = c0 + ci;
@@ -194,7 +204,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
     const int rem = mine ? D * E * 2 - 64 * c : 0;
     const i32x4 r1 = make_rsrc_words(W1h + (size_t)c * 32, rem > 0 ? rem : 0);
     const i32x4 r2 = make_rsrc_words(W2h + (size_t)c * 32 * D, clamp0(lim, 32) * D * 2);
-    const int slot = RB + (ci & (DX_NSLOT - 1)) * (int)SLOT + wp * 1024;
+    const int slot = RB + (ci & (NSL - 1)) * (int)SLOT + wp * 1024;
 #pragma unroll
     for (int k = 0; k < NDMA; ++k) {
       // W1c or W2c piece (wave-uniform): word-wise selects keep the loop body one basic block
@@ -252,7 +262,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
   auto mfma_phase = [&](auto G2, int c) {
     constexpr bool DO_G2 = decltype(G2)::value;
     constexpr int M2 = DO_G2 ? N2 : 0, NOPS = N1 + M2;
-    const int base1 = RB + (c & (DX_NSLOT - 1)) * (int)SLOT, base2 = RB + ((c - 1) & (DX_NSLOT - 1)) * (int)SLOT;
+    const int base1 = RB + (c & (NSL - 1)) * (int)SLOT, base2 = RB + ((c - 1) & (NSL - 1)) * (int)SLOT;
     auto fetch = [&](int j) -> u32x4 {
       const int q = sched_index(j, N1, M2);
       if (sched_is_g2(j, N1, M2)) {
@@ -285,7 +295,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
     }
   };
   auto g2_only = [&](int c) {  // dX += dZ(c) W1c(c)^T
-    const int base2 = RB + (c & (DX_NSLOT - 1)) * (int)SLOT;
+    const int base2 = RB + (c & (NSL - 1)) * (int)SLOT;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
@@ -300,12 +310,12 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
                                 act_b<ACT>(z[8 * s2 + 2 * w + 1], dh[8 * s2 + 2 * w + 1]));
     __builtin_amdgcn_sched_barrier(0);
   };
-  // iteration c requests chunk c + DX_PF; the end-of-chunk barrier publishes chunk c + 1 (each
+  // iteration c requests chunk c + PF; the end-of-chunk barrier publishes chunk c + 1 (each
   // wave waits for its own pieces first) and retires every read of chunk c - 1, whose slot
-  // holds chunk c - 1 + DX_NSLOT later
-  auto chunk_begin = [&](int c) { dma_chunk(c + DX_PF); };
+  // holds chunk c - 1 + NSL later
+  auto chunk_begin = [&](int c) { dma_chunk(c + PF); };
   auto chunk_end = [&]() {
-    wait_vmcnt<NDMA * (DX_PF - 1)>();
+    wait_vmcnt<NDMA * (PF - 1)>();
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
     asm volatile("" ::: "memory");       // keep LDS accesses on their side of the barrier
     __builtin_amdgcn_s_barrier();
@@ -313,7 +323,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
   };
 
 #pragma unroll
-  for (int c = 0; c < DX_PF; ++c) dma_chunk(c);
+  for (int c = 0; c < PF; ++c) dma_chunk(c);
   chunk_end();
   const std::true_type T{};
   const std::false_type F{};
@@ -369,7 +379,7 @@ __device__ __forceinline__ void dx2_body(const u16* __restrict__ X, const u16* _
       }
   }
   if (pws != nullptr)
-    store_rows<BF16, D>(acc, pws, 0, B - bt * dx2_rows<D, DES>(), wp * 32, g, l32, 1);
+    store_rows<BF16, D>(acc, pws, 0, B - bt * ROWS, wp * 32, g, l32, 1);
   else
     store_rows<BF16, D>(acc, dX, (size_t)h * B * D, B, b_wave, g, l32, outf32);
 }
@@ -718,6 +728,17 @@ dx2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
            const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
   dx2_body<BF16, D, ACT, DES>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32, xcd_remap(blockIdx.x, gridDim.x), 0,
                               (E + 31) >> 5, nullptr);
+}
+
+// dX programs at D = 256 (the tuned backward's dX only; its dW runs on the generic kernels):
+// 4 waves of 32 rows, one per SIMD (the X and dO rows and the dX accumulators take ~320
+// registers of the 512).
+template <bool BF16, int ACT>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+dx256_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+             const u16* __restrict__ dO, void* __restrict__ dX, int B, int E, int tiles_per_head, int outf32) {
+  dx2_body<BF16, 256, ACT, 1, 4>(X, W1, W2, dO, dX, B, E, tiles_per_head, outf32, xcd_remap(blockIdx.x, gridDim.x),
+                                 0, (E + 31) >> 5, nullptr);
 }
 
 template <bool BF16, int D, int ACT, bool HILO, bool DZ, int ET = DW_ET>
@@ -1394,6 +1415,35 @@ static hipError_t launch_bwd_a(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     case ACT_SIGMOID: return launch_bwd_e<BF16, D, ACT_SIGMOID>(a, p, st);
     default: return launch_bwd_e<BF16, D, ACT_NONE>(a, p, st);
   }
+}
+
+template <bool BF16, int ACT>
+static hipError_t launch_dx256_t(const BwdArgs& a, hipStream_t st) {
+  const long long tph = (a.B + 127) / 128, grid = tph * a.H;
+  if (grid <= 0) return hipSuccess;
+  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  constexpr size_t lds = (size_t)dx_nslot(256) * 128u * 256u;
+  auto k = dx256_kernel<BF16, ACT>;
+  static std::atomic<unsigned long long> lds_set{0};
+  hipError_t e = set_lds_once((const void*)k, (int)lds, lds_set);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(256), lds, st, (const u16*)a.x, (const u16*)a.w1, (const u16*)a.w2,
+                     (const u16*)a.dout, a.dx, (int)a.B, (int)a.E, (int)tph, a.out_f32 ? 1 : 0);
+  return hipGetLastError();
+}
+
+template <bool BF16>
+static hipError_t launch_dx256_a(const BwdArgs& a, hipStream_t st) {
+  switch (a.act) {
+    case ACT_SILU: return launch_dx256_t<BF16, ACT_SILU>(a, st);
+    case ACT_LEAKY: return launch_dx256_t<BF16, ACT_LEAKY>(a, st);
+    case ACT_SIGMOID: return launch_dx256_t<BF16, ACT_SIGMOID>(a, st);
+    default: return launch_dx256_t<BF16, ACT_NONE>(a, st);
+  }
+}
+
+hipError_t launch_dx256(const BwdArgs& a, hipStream_t st) {
+  return a.bf16 ? launch_dx256_a<true>(a, st) : launch_dx256_a<false>(a, st);
 }
 
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {

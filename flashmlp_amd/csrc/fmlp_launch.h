@@ -147,6 +147,9 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t st);
 hipError_t launch_tile_reduce(const float* ws, void* out, bool bf16, int B, int D, int BB, int H, int T, int xs,
                               int n_split, int outf32, hipStream_t st);
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st);
+// dX alone at D = 256 (dense 16-bit, E % 8 == 0): the tuned dX programs; the caller runs dW on
+// the generic kernels
+hipError_t launch_dx256(const BwdArgs& a, hipStream_t st);
 
 // The library's static device scratch (fmlp_bwd_noalloc): its device address on the current
 // device, looked up once per device, and its size in bytes.

@@ -1,12 +1,16 @@
-"""The tuned forward at D = 256 (fwd_kernel with four waves of 32 rows, one per SIMD; dense 16-bit
-tensors with E % 8 == 0; the backward of such shapes runs on the generic kernels).
+"""The tuned kernels at D = 256: the forward (fwd_kernel with four waves of 32 rows, one per SIMD)
+and the backward's dX programs (dx256_kernel, the same layout), for dense 16-bit tensors with
+E % 8 == 0; the backward's dW runs on the generic kernels there.
 
 Each case checks through the C ABI:
   * the fp32 sums (FMLP_OUT_F32) against the oracle's cast-point emulation at the north star's
     1e-4, and against the generic kernel's sums for the same values passed as a non-dense view
     (so the generic path takes them) within 1e-5 (summation order only);
   * the io output against the fp32 autograd oracle at the parity bar (3e-2 + 3e-2 |ref|),
-    every element written (output NaN-filled first).
+    every element written (output NaN-filled first);
+  * for the backward, dX's fp32 sums against the emulation and the generic kernel likewise, dW
+    bitwise equal to the all-generic backward's, and the partial backwards (FMLP_BWD_NO_DW,
+    FMLP_BWD_NO_DX) bitwise equal to the full one.
 """
 import ctypes
 import sys
@@ -107,3 +111,62 @@ def test_tuned_forward_d256_larger_and_split():
     rel = _normrel(o.cpu(), e)
     _say(f"[fwd-d256] split fp32 sums rel {rel:.3g}")
     assert torch.isfinite(o).all() and rel <= 1e-4
+
+
+def _bwd(x, w1, w2, do, act, code, out_dtype, strided=False):
+    L = _lib.lib()
+    H, B, D = x.shape
+    E = w1.shape[2]
+    dx = torch.full((H, B, D), float("nan"), dtype=out_dtype, device=x.device)
+    dw1 = torch.full((H, D, E), float("nan"), dtype=out_dtype, device=x.device)
+    dw2 = torch.full((H, E, D), float("nan"), dtype=out_dtype, device=x.device)
+    n = L.fmlp_bwd_workspace_bytes(H, B, D, E, code)
+    ws = torch.empty(max(n, 16), dtype=torch.uint8, device=x.device)
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    a = _lib.ACT_CODES[act]
+    st = L.fmlp_bwd_strided(_ptr(x), _ptr(w1), _ptr(w2), _ptr(do), _ptr(dx), _ptr(dw1), _ptr(dw2), H, B, D, E,
+                            _lib.strides(x), _lib.strides(w1), _lib.strides(w2), _lib.strides(do), code, a, _ptr(ws),
+                            n, stream)
+    _lib.check(st, "backward")
+    torch.cuda.synchronize()
+    return dx, dw1, dw2
+
+
+BWD_CASES = [(torch.float16, "silu", 2, 300, 136), (torch.bfloat16, "sigmoid", 2, 300, 136),
+             (torch.bfloat16, "leaky_relu", 3, 1000, 512), (torch.float16, "", 2, 129, 264)]
+
+
+@pytest.mark.parametrize("dt,act,H,B,E", BWD_CASES, ids=[f"{str(c[0]).split('.')[-1]}-{c[1] or 'linear'}-B{c[3]}"
+                                                          for c in BWD_CASES])
+def test_tuned_dx_d256(dt, act, H, B, E):
+    D = 256
+    code = _DT[dt]
+    _say(f"[bwd-d256] H={H} B={B} D={D} E={E} {dt} act='{act}'")
+    x, w1, w2, do = make_inputs(H, B, D, E, dt, 1.0, seed=31)
+    xd, w1d, w2d, dod = (t.cuda() for t in (x, w1, w2, do))
+    xpad = torch.zeros(H, B, D + 8, dtype=dt, device="cuda")
+    xpad[:, :, :D] = xd
+    xv = xpad[:, :, :D]  # a non-dense view: the whole backward on the generic kernels
+
+    s = _bwd(xd, w1d, w2d, dod, act, code | _lib.FMLP_OUT_F32, torch.float32)
+    sg = _bwd(xv, w1d, w2d, dod, act, code | _lib.FMLP_OUT_F32, torch.float32)
+    e = emulate.emu_bwd(x, w1, w2, do, act, dt, round_out=False)
+    rel = {k: _normrel(g.cpu(), r) for k, g, r in zip(("dx", "dw1", "dw2"), s, e)}
+    rel_g = _normrel(s[0], sg[0])
+    sums = " ".join(f"{k}={v:.3g}" for k, v in rel.items())
+    _say(f"[bwd-d256] fp32 sums rel {sums}, dx to generic {rel_g:.3g}")
+    assert max(rel.values()) <= 1e-4 and rel_g <= 1e-5
+    for a_, b_ in zip(s[1:], sg[1:]):  # dW: the same generic kernels either way
+        assert torch.equal(a_, b_)
+
+    dx, dw1, dw2 = _bwd(xd, w1d, w2d, dod, act, code, dt)
+    _, rdx, _, _ = reference.autograd_grads(x, w1, w2, do, act)
+    bad = ((dx.cpu().float() - rdx).abs() > 3e-2 + 3e-2 * rdx.abs()).sum().item()
+    _say(f"[bwd-d256] dx outside 3e-2: {bad}")
+    assert torch.isfinite(dx.float()).all() and bad == 0
+    # partial backwards: the same programs, bitwise
+    dxo, _, _ = _bwd(xd, w1d, w2d, dod, act, code | _lib.FMLP_BWD_NO_DW, dt)
+    _, dw1o, dw2o = _bwd(xd, w1d, w2d, dod, act, code | _lib.FMLP_BWD_NO_DX, dt)
+    assert torch.equal(dx.view(torch.int16), dxo.view(torch.int16))
+    assert torch.equal(dw1.view(torch.int16), dw1o.view(torch.int16))
+    assert torch.equal(dw2.view(torch.int16), dw2o.view(torch.int16))
