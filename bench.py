@@ -21,8 +21,9 @@ The default (cfg4) line also carries, measured in the same process after the hea
     the form the north star names), with the dW accuracy mode (accurate_dw=True: dW within the
     elementwise tolerance of fp32), and with both;
   * `configs`: every other BASELINE.json configuration (cfg2, cfg3, cfg5 sigmoid and linear,
-    the forward-only cfg5s sweep) on the tuned kernels, and two shapes of the generic kernels
-    (the reference's CPU configuration cfg1 in fp32, and D = 256);
+    the forward-only cfg5s sweep) on the tuned kernels, and two shapes outside the tuned
+    kernels' main range: the reference's CPU configuration cfg1 in fp32 (generic kernels) and
+    D = 256 (tuned forward and dX programs, generic dW programs);
   * `vs_pytorch_unfused`: the unfused PyTorch path (bmm -> activation -> bmm, the (H, B, E)
     intermediates kept, manual backward) on the same GPU against FlashMLP, at cfg4 and at the
     four shapes of the reference's performance.md (example.py:98-135 compares the two);
@@ -66,7 +67,8 @@ WORKLOADS = {
     "cfg5": (8, 4097, 64, 2048, "f16", "sigmoid", 2.0, False),
     "cfg5_linear": (8, 4097, 64, 2048, "f16", "", 2.0, False),
     "cfg5s": (8, 65536, 64, 2048, "f16", "sigmoid", 2.0, True),
-    # generic kernels: the reference's CPU configuration in fp32, D = 256
+    # the reference's CPU configuration in fp32 (generic kernels), and
+    # D = 256 (tuned forward and dX programs, generic dW programs)
     "cfg1_fp32": (12, 1024, 64, 768, "f32", "silu", 1.0, False),
     "d256": (8, 4096, 256, 1024, "bf16", "silu", 1.0, False),
 }
@@ -386,7 +388,8 @@ def _bwd_form(H, B, D, E, dt_name, act, accurate_dw=False, recompute=False):
 
     code = {"bf16": _lib.FMLP_DTYPE_BF16, "f16": _lib.FMLP_DTYPE_F16, "f32": _lib.FMLP_DTYPE_F32}[dt_name]
     if not _lib.lib().fmlp_shape_tuned(D, E, code):
-        return "generic"
+        # dense 16-bit D = 256 (E % 8 == 0): tuned dX programs next to the generic dW programs
+        return "dx256+generic-dw" if D == 256 and dt_name != "f32" and E % 8 == 0 else "generic"
     code |= (_lib.FMLP_DW_HILO if accurate_dw else 0) | (_lib.FMLP_BWD_RECOMPUTE if recompute else 0)
     return "stored-dZ" if _lib.lib().fmlp_bwd_stores_dz(H, B, D, E, code, _lib.ACT_CODES[act]) else "recompute"
 
@@ -711,7 +714,8 @@ def main():
         line["bwd_form"] = form
         kernels = {"stored-dZ": "fmlp::dw2_kernel (storing dZ), fmlp::dxg_kernel",
                    "recompute": "fmlp::bwd_kernel (dW and dX programs)",
-                   "generic": "fmlp::gen_dw_kernel, fmlp::gen_dx_kernel"}[form]
+                   "generic": "fmlp::gen_dw_kernel, fmlp::gen_dx_kernel",
+                   "dx256+generic-dw": "fmlp::dx256_kernel, fmlp::gen_dw_kernel"}[form]
         line["roofline"] = {
             "kernel": f"fmlp_bwd ({form}): {kernels}",
             "bound": "mfma",
