@@ -388,8 +388,8 @@ def _bwd_form(H, B, D, E, dt_name, act, accurate_dw=False, recompute=False):
 
     code = {"bf16": _lib.FMLP_DTYPE_BF16, "f16": _lib.FMLP_DTYPE_F16, "f32": _lib.FMLP_DTYPE_F32}[dt_name]
     if not _lib.lib().fmlp_shape_tuned(D, E, code):
-        # dense 16-bit D = 256 (E % 8 == 0): tuned dX programs next to the generic dW programs
-        return "dx256+generic-dw" if D == 256 and dt_name != "f32" and E % 8 == 0 else "generic"
+        # dense 16-bit D = 256 (E % 8 == 0): the D = 256 dX and dW programs
+        return "dx256+dw256" if D == 256 and dt_name != "f32" and E % 8 == 0 else "generic"
     code |= (_lib.FMLP_DW_HILO if accurate_dw else 0) | (_lib.FMLP_BWD_RECOMPUTE if recompute else 0)
     return "stored-dZ" if _lib.lib().fmlp_bwd_stores_dz(H, B, D, E, code, _lib.ACT_CODES[act]) else "recompute"
 
@@ -715,7 +715,7 @@ def main():
         kernels = {"stored-dZ": "fmlp::dw2_kernel (storing dZ), fmlp::dxg_kernel",
                    "recompute": "fmlp::bwd_kernel (dW and dX programs)",
                    "generic": "fmlp::gen_dw_kernel, fmlp::gen_dx_kernel",
-                   "dx256+generic-dw": "fmlp::dx256_kernel, fmlp::gen_dw_kernel"}[form]
+                   "dx256+dw256": "fmlp::dx256_kernel, fmlp::dw256_kernel"}[form]
         line["roofline"] = {
             "kernel": f"fmlp_bwd ({form}): {kernels}",
             "bound": "mfma",

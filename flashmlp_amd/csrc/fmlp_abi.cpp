@@ -94,7 +94,8 @@ size_t elem_bytes(int io) { return io == FMLP_DTYPE_F32 ? 4 : 2; }
 bool tuned_shape(int64_t D, int64_t E, int io) {
   return (io == FMLP_DTYPE_F16 || io == FMLP_DTYPE_BF16) && (D == 64 || D == 128) && E % 8 == 0;
 }
-// the tuned forward also takes D = 256 (one wave per SIMD); the backward runs it generically
+// the tuned forward also takes D = 256 (one wave per SIMD), and so do the backward's D = 256 dX
+// and dW programs (launch_dx256, launch_dw256), with the generic kernels' workspace rule
 bool fwd_tuned_shape(int64_t D, int64_t E, int io) {
   return tuned_shape(D, E, io) || ((io == FMLP_DTYPE_F16 || io == FMLP_DTYPE_BF16) && D == 256 && E % 8 == 0);
 }
@@ -309,8 +310,14 @@ FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int
   if (dtype & FMLP_BWD_NO_DW) return 0;            // the dX programs alone use no workspace
   int cus = 0;
   if (num_cus_current(&cus) != FMLP_OK) return 0;
-  // the generic kernels: the fp32 partials of their dW programs' B split
-  if (!tuned_shape(D, E, io_of(dtype))) return fmlp::gen_plan(H, B, D, E, cus, (size_t)-1).ws_bytes;
+  // the generic kernels: the fp32 partials of their dW programs' B split; dense 16-bit D = 256
+  // with E % 8 == 0 runs the D = 256 dW programs, whose split may need more
+  if (!tuned_shape(D, E, io_of(dtype))) {
+    const size_t g = fmlp::gen_plan(H, B, D, E, cus, (size_t)-1).ws_bytes;
+    if (!fwd_tuned_shape(D, E, io_of(dtype))) return g;
+    const size_t w = fmlp::plan_dw256(H, B, E, (dtype & FMLP_DW_HILO) != 0, cus, (size_t)-1).ws_bytes;
+    return w > g ? w : g;
+  }
   // the plan depends on the activation, which this query does not take: the largest over them
   size_t n = 0;
   for (int act = 0; act < 4; ++act) {
@@ -326,10 +333,20 @@ FMLP_EXPORT int fmlp_bwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int dt
   int st = check_shape(H, B, D, E, dtype);
   if (st) return st;
   if ((st = check_act(act))) return st;
-  if (!tuned_shape(D, E, io_of(dtype))) return fail(FMLP_ERR_UNSUPPORTED, "the generic kernels have no such plan");
+  if (!fwd_tuned_shape(D, E, io_of(dtype))) return fail(FMLP_ERR_UNSUPPORTED, "the generic kernels have no such plan");
   if (n_info > 0 && info == nullptr) return fail(FMLP_ERR_INVALID_ARG, "info is NULL");
   int cus = 0;
   if ((st = num_cus_current(&cus))) return st;
+  if (!tuned_shape(D, E, io_of(dtype))) {
+    // D = 256: the dX programs (128 rows each) and the dW programs' split with an unlimited
+    // workspace (a call splits B only as far as its workspace holds)
+    const bool no_dw = (dtype & FMLP_BWD_NO_DW) != 0, no_dx = (dtype & FMLP_BWD_NO_DX) != 0;
+    const fmlp::Dw256Plan w = fmlp::plan_dw256(H, B, E, (dtype & FMLP_DW_HILO) != 0, cus, (size_t)-1);
+    const int64_t v[11] = {0, no_dw ? 1 : w.nS, 1, 0, 0, no_dw ? 0 : w.n, no_dx ? 0 : H * ((B + 127) / 128), 0,
+                           no_dw ? 0 : (int64_t)w.ws_bytes, act, 128};
+    for (int i = 0; i < n_info && i < 11; ++i) info[i] = v[i];
+    return ok();
+  }
   const fmlp::BwdPlan p = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus);
   const int64_t v[11] = {p.dz ? 1 : 0, p.nS, p.dx_es, p.dxs_xs, p.dx_first ? 1 : 0, p.n_dw,
                          p.n_dx, p.n_dxs, (int64_t)p.ws_bytes, act, p.et_w};
@@ -398,6 +415,30 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
     fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io == FMLP_DTYPE_BF16, act, ws,
                     (dtype & FMLP_OUT_F32) != 0, (dtype & FMLP_DW_HILO) != 0, want_dx, want_dw};
     e = fmlp::launch_bwd(a, plan, (hipStream_t)stream);
+  } else if (dense && aligned && fwd_tuned_shape(D, E, io)) {
+    // dense 16-bit D = 256 with E % 8 == 0: the D = 256 dX and dW programs; as on the generic
+    // kernels, the dW programs split B only as far as the given workspace (or the static
+    // scratch) holds their partials
+    void* ws = nullptr;
+    fmlp::Dw256Plan wp{};
+    if (want_dw) {
+      int cus = 0;
+      if ((st = num_cus_current(&cus))) return st;
+      const size_t room = noalloc ? fmlp::kScratchBytes
+                                  : (workspace != nullptr && aligned16(workspace) ? workspace_bytes : 0);
+      wp = fmlp::plan_dw256(H, B, E, (dtype & FMLP_DW_HILO) != 0, cus, room);
+      if (wp.ws_bytes > 0) {
+        ws = workspace;
+        if (noalloc) {
+          e = fmlp::scratch_current_device(&ws);
+          if (e != hipSuccess) return fail(FMLP_ERR_HIP, "scratch lookup: %s", hipGetErrorString(e));
+        }
+      }
+    }
+    fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io == FMLP_DTYPE_BF16, act, ws,
+                    (dtype & FMLP_OUT_F32) != 0, (dtype & FMLP_DW_HILO) != 0, want_dx, want_dw};
+    if (want_dx) e = fmlp::launch_dx256(a, (hipStream_t)stream);
+    if (e == hipSuccess && want_dw) e = fmlp::launch_dw256(a, wp, (hipStream_t)stream);
   } else {
     fmlp::GenArgs g = gen_args(x, w1, w2, dout, nullptr, dx, dw1, dw2, H, B, D, E, dtype, act);
     g.want_dx = want_dx ? 1 : 0;
@@ -435,15 +476,7 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
         g.ws = ws;
       }
     }
-    // dense 16-bit D = 256 with E % 8 == 0: dX on the tuned dX programs, dW on the generic kernels
-    const bool dx256 = want_dx && dense && aligned && fwd_tuned_shape(D, E, io) && !tuned_shape(D, E, io);
-    if (dx256) {
-      fmlp::BwdArgs a{x, w1, w2, dout, dx, dw1, dw2, H, B, D, E, io == FMLP_DTYPE_BF16, act, nullptr,
-                      (dtype & FMLP_OUT_F32) != 0, false, true, false};
-      e = fmlp::launch_dx256(a, (hipStream_t)stream);
-      g.want_dx = 0;
-    }
-    if (e == hipSuccess && (g.want_dx || g.want_dw)) e = fmlp::launch_gen_bwd(g, (hipStream_t)stream);
+    e = fmlp::launch_gen_bwd(g, (hipStream_t)stream);
   }
   if (e != hipSuccess) return fail(FMLP_ERR_HIP, "backward launch: %s", hipGetErrorString(e));
   return ok();

@@ -741,6 +741,259 @@ dx256_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* _
                                  0, (E + 31) >> 5, nullptr);
 }
 
+// ------------------------------------------------------------------------------------
+// dW programs at D = 256 (dw256_kernel): 4 waves, one per SIMD. A program owns 128 E-columns
+// of one head (wave w the 32 columns e0 = e_prog + 32 w) and a B-range of rows_per_split
+// rows, as a dw2_body program does. The 512 registers of a lone wave hold its two
+// accumulators (dW2 and dW1^T, [32 e][256 d] each: 256) and, loaded once, its weight operands:
+// the B operands of Z = X W1c and dH = dO W2c^T for its columns (lane = column e0 + l32,
+// k-slots d = 16 ks + 8 g + j; 128). Only X and dO pass through LDS: per 32-row subtile
+// 32 KB in a 4-slot ring filled by buffer-to-LDS loads DW4_PF subtiles ahead and read by all
+// four waves. Per subtile a wave issues 64 MFMAs in one operand stream:
+//   Z = X W1c (16, a chain), dH = dO W2c^T (16) with h = act(Z) and act'(Z) of elements
+//   0-11 between them, dW2 += h^T dO (16) with elements 12-15 and then dZ = dH act'(Z)
+//   between them, dW1^T += dZ^T X (16)
+// (the dW products twice with HILO). Subtile layout and operand reads are dw2_body's
+// (w2s_off blocks; row reads for the A operands of Z and dH, ds_read_b64_tr_b16 for the B
+// operands of the dW products). W1c reaches its register layout through LDS once: a
+// row-major [256 d][128 e] staging tile in the ring's last two slots, read transposed before
+// the ring first uses them; W2c rows are loaded straight into registers.
+// ------------------------------------------------------------------------------------
+constexpr int DW4_NSLOT = 4;                   // subtile ring slots
+constexpr int DW4_PF = 3;                      // subtiles requested ahead of the one read
+constexpr int DW4_SUB = 32 * 256 * 2;          // bytes of one [32][256] tile (X or dO)
+constexpr int DW4_SLOT = 2 * DW4_SUB;          // a slot: the X tile, then the dO tile
+constexpr int DW4_NPL = DW4_SLOT / 16 / 256;   // 16-byte pieces per lane per subtile
+constexpr int DW4_PD = 3;                      // operand reads ahead of their MFMA
+static_assert(DW4_PF <= DW4_NSLOT - 1, "a slot is reloaded only after the barrier that retires its last reader");
+static_assert(DW4_PF >= 2 && 2 * DW4_SLOT == 256 * DW_ET * 2, "the W1c staging tile fills the ring's last two slots");
+static_assert(16 % (DW4_PD + 1) == 0, "each 16-step group starts at ring slot 0");
+
+// h = act(z) and the factor f with dZ = dH f (act_fb's arithmetic, split in two so that h can be
+// computed before dH is)
+template <int ACT>
+__device__ __forceinline__ void act_hf(float z, float& h, float& f) {
+  if constexpr (ACT == ACT_SILU) {
+    const float s = sigm(z);
+    h = z * s;
+    f = __builtin_fmaf(h, 1.0f - s, s);
+  } else if constexpr (ACT == ACT_LEAKY) {
+    const bool p = z > 0.f;
+    h = p ? z : 0.01f * z;
+    f = p ? 1.0f : 0.01f;
+  } else if constexpr (ACT == ACT_SIGMOID) {
+    const float s = sigm(z);
+    h = s;
+    f = s - s * s;
+  } else {
+    h = z;
+    f = 1.0f;
+  }
+}
+
+template <bool BF16, int ACT, bool HILO>
+__global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+dw256_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
+             const u16* __restrict__ dO, void* __restrict__ dW1, void* __restrict__ dW2, float* __restrict__ ws,
+             int H, int B, int E, int nE, int nS, int rows_per_split, int outf32) {
+  constexpr int D = 256, KS = D / 16, NTN = D / 32;
+  constexpr int STG = 2 * DW4_SLOT;  // W1c staging tile: [256 d][128 e], 256-byte rows
+  constexpr int PD = DW4_PD;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int G = lane >> 4, i16 = lane & 15, g = lane >> 5, l32 = lane & 31;
+  const int t = xcd_remap(blockIdx.x, gridDim.x);
+  const int et = t % nE, hs = t / nE;
+  const int s = hs % nS, h = hs / nS;
+  const int e_prog = et * DW_ET, e0 = e_prog + 32 * wave;
+  const int b_lo = s * rows_per_split;
+  const int b_hi = min(B, b_lo + rows_per_split);
+  const int nsub = b_hi > b_lo ? (b_hi - b_lo + DW_BT - 1) / DW_BT : 0;
+
+  const u16* Xh = X + (size_t)h * B * D;
+  const u16* dOh = dO + (size_t)h * B * D;
+  const u16* W1h = W1 + (size_t)h * D * E;
+  const u16* W2h = W2 + (size_t)h * E * D;
+
+  // ---- subtile loads: lane-linear 16-byte pieces (pieces k4 of the X tile, then of dO) ----
+  unsigned pieceOff[4];
+#pragma unroll
+  for (int k4 = 0; k4 < 4; ++k4) {
+    const unsigned pr = k4 * 256 + wave * 64 + lane, o = 16u * pr, r = (o % 2048u) / 64u;
+    const unsigned q = 4u * (o / 2048u) + (((o / 16u) & 3u) ^ ((r >> 2) & 3u));
+    pieceOff[k4] = r * (D * 2u) + q * 16u;
+  }
+  // subtile i (rows b_lo + 32 i ..) into slot i % 4; rows at or past b_hi read as zeros (an
+  // empty resource past the range), which add nothing to either product
+  auto issue = [&](int i) {
+    const int slot = i & (DW4_NSLOT - 1);
+    const int r0 = b_lo + i * DW_BT;
+    const int bytes = clamp0(b_hi - r0, DW_BT) * D * 2;
+    const i32x4 rx = make_rsrc_words(Xh + (size_t)r0 * D, bytes);
+    const i32x4 rd = make_rsrc_words(dOh + (size_t)r0 * D, bytes);
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4)
+      buf_load16_lds(rx, pieceOff[k4], slot * DW4_SLOT + 16 * (k4 * 256 + wave * 64));
+#pragma unroll
+    for (int k4 = 0; k4 < 4; ++k4)
+      buf_load16_lds(rd, pieceOff[k4], slot * DW4_SLOT + DW4_SUB + 16 * (k4 * 256 + wave * 64));
+  };
+  issue(0);
+  issue(1);
+
+  // ---- weight operands (once) ----
+  // W1 rows d, columns e_prog .. + 127 -> staging tile (zeros past E; E % 8 == 0)
+#pragma unroll 4
+  for (int k = 0; k < 256 * 16 / 256; ++k) {
+    const int p = tid + 256 * k, d = p >> 4, u = p & 15;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (e_prog + 8 * u < E) v = *(const u32x4*)(W1h + (size_t)d * E + e_prog + 8 * u);
+    lds_write16(STG + d * 256 + u * 16, v);
+  }
+  // W2 row e0 + l32, d = 16 ks + 8 g .. + 7: the B operand of dH as it lies in memory
+  u32x4 w2op[KS];
+  const bool col_ok = e0 + l32 < E;
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (col_ok) v = *(const u32x4*)(W2h + (size_t)(e0 + l32) * D + 16 * ks + 8 * g);
+    w2op[ks] = v;
+  }
+  __syncthreads();
+  // W1c B operand: ds_read_b64_tr_b16 over 4 rows d x 16 columns e of the staging tile gives
+  // lane i16 of each 16-lane group column 32 wave + 16 (G & 1) + i16, rows d .. d + 3
+  u32x4 w1op[KS];
+  {
+    const int c2 = (32 * wave + 16 * (G & 1) + 4 * (i16 & 3)) * 2;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int d0 = 16 * ks + 8 * g + (i16 >> 2);
+      w1op[ks] = cat(lds_read_tr(STG + d0 * 256 + c2), lds_read_tr(STG + (d0 + 4) * 256 + c2));
+    }
+  }
+  // the staging reads have returned (lgkmcnt 0) and subtiles 0 and 1 have landed before the
+  // barrier that hands the staging slots to the ring
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  wait_vmcnt<0>();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int i = 2; i < DW4_PF; ++i) issue(i);
+
+  // ---- per-lane LDS offsets inside a slot ----
+  //   A operand of Z / dH: row l32, piece 2 ks + g -> offRow[ks % 2] + (ks / 2) * 2048
+  int offRow[2];
+#pragma unroll
+  for (int kp = 0; kp < 2; ++kp) offRow[kp] = (int)w2s_off(l32, 2 * kp + g);
+  //   B operand of dW2 / dW1^T (transposed reads) -> offTr[r] + nt * 2048 + s2 * 1024
+  int offTr[2];
+#pragma unroll
+  for (int r = 0; r < 2; ++r)
+    offTr[r] = (int)(w2s_off(8 * r + 4 * g + (i16 >> 2), 2 * (G & 1) + ((i16 & 3) >> 1)) + 8u * (i16 & 1));
+
+  f32x16 a2[NTN], a1[NTN];
+#pragma unroll
+  for (int nt = 0; nt < NTN; ++nt) {
+    a2[nt] = zero16();
+    a1[nt] = zero16();
+  }
+  f32x16 z = zero16(), dh = zero16();
+  u32x4 hT[2], dzT[2], hL[2], dzL[2];  // lo terms: HILO only
+
+  for (int i = 0; i < nsub; ++i) {
+    issue(i + DW4_PF);  // into the slot of subtile i - 1, retired by the last barrier
+    const int base = (i & (DW4_NSLOT - 1)) * DW4_SLOT;
+    // operand q of the subtile's 64 MFMAs: X rows (Z), dO rows (dH), dO^T (dW2), X^T (dW1^T)
+    auto fetch = [&](int q) -> u32x4 {
+      if (q < 32) {
+        const int ks = q & 15;
+        return lds_read16(base + (q < 16 ? 0 : DW4_SUB) + offRow[ks & 1] + (ks >> 1) * 2048);
+      }
+      const int qq = q & 15, s2 = qq >> 3, nt = qq & 7;
+      const int bb = base + (q < 48 ? DW4_SUB : 0) + nt * 2048 + s2 * 1024;
+      return cat(lds_read_tr(bb + offTr[0]), lds_read_tr(bb + offTr[1]));
+    };
+    float hv[16], fv[16], dv[16];
+    auto vh = [&](int e) {  // h and act' of element e
+      act_hf<ACT>(z[e], hv[e], fv[e]);
+      if (e & 1) {
+        const unsigned ph = pack2<BF16>(hv[e - 1], hv[e]);
+        hT[e >> 3][(e >> 1) & 3] = ph;
+        if constexpr (HILO)  // v - round(v) is exact in fp32; its rounding is the lo term
+          hL[e >> 3][(e >> 1) & 3] = pack2<BF16>(hv[e - 1] - lo_f32<BF16>(ph), hv[e] - hi_f32<BF16>(ph));
+      }
+    };
+    auto vd = [&](int e) {  // dZ of element e
+      dv[e] = dh[e] * fv[e];
+      if (e & 1) {
+        const unsigned pd = pack2<BF16>(dv[e - 1], dv[e]);
+        dzT[e >> 3][(e >> 1) & 3] = pd;
+        if constexpr (HILO)
+          dzL[e >> 3][(e >> 1) & 3] = pack2<BF16>(dv[e - 1] - lo_f32<BF16>(pd), dv[e] - hi_f32<BF16>(pd));
+      }
+    };
+    u32x4 ring[PD + 1];
+#pragma unroll
+    for (int j = 0; j < PD; ++j) ring[j] = fetch(j);
+    __builtin_amdgcn_sched_barrier(0);
+    // four groups of 16 steps (each loop unrolls fully, so every index below is a constant);
+    // step q takes ring slot q % 4 (16 is a multiple of PD + 1) and reads operand q + PD
+    auto next = [&](int q) {
+      if (q + PD < 64) ring[(q + PD) % (PD + 1)] = fetch(q + PD);
+    };
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {  // Z = X W1c
+      const u32x4 op = ring[k % (PD + 1)];
+      next(k);
+      z = mfma<BF16>(op, w1op[k], k == 0 ? zero16() : z);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {  // dH = dO W2c^T; h and act' of elements 0-11
+      const u32x4 op = ring[k % (PD + 1)];
+      next(16 + k);
+      dh = mfma<BF16>(op, w2op[k], k == 0 ? zero16() : dh);
+#pragma unroll
+      for (int e = sched_elem_begin(k, 16, 12); e < sched_elem_begin(k + 1, 16, 12); ++e) vh(e);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {  // dW2 += h^T dO; elements 12-15, then dZ
+      const u32x4 op = ring[k % (PD + 1)];
+      next(32 + k);
+      const int s2 = k >> 3, nt = k & 7;
+      a2[nt] = mfma<BF16>(hT[s2], op, a2[nt]);
+      if constexpr (HILO) a2[nt] = mfma<BF16>(hL[s2], op, a2[nt]);
+      if (k < 8) {
+#pragma unroll
+        for (int e = 12 + sched_elem_begin(k, 8, 4); e < 12 + sched_elem_begin(k + 1, 8, 4); ++e) vh(e);
+      } else {
+#pragma unroll
+        for (int e = sched_elem_begin(k - 8, 8, 16); e < sched_elem_begin(k - 7, 8, 16); ++e) vd(e);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {  // dW1^T += dZ^T X
+      const u32x4 op = ring[k % (PD + 1)];
+      next(48 + k);
+      const int s2 = k >> 3, nt = k & 7;
+      a1[nt] = mfma<BF16>(dzT[s2], op, a1[nt]);
+      if constexpr (HILO) a1[nt] = mfma<BF16>(dzL[s2], op, a1[nt]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // subtile i + 1 has landed (this wave's part; the barrier publishes the others' and retires
+    // every read of slot i, which subtile i + 4 reuses)
+    wait_vmcnt<(DW4_PF - 1) * DW4_NPL>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  wait_vmcnt<0>();  // the empty requests past the range
+  dw_store<BF16, D>(a1, a2, dW1, dW2, ws, H, E, h, s, nS, e0, g, l32, outf32);
+}
+
 template <bool BF16, int D, int ACT, bool HILO, bool DZ, int ET = DW_ET>
 __global__ void __launch_bounds__(DW2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 dw2_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
@@ -1297,10 +1550,60 @@ BwdPlan plan_bwd(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo,
   return p;
 }
 
+// B split of the D = 256 dW programs: the nS (1, 2, 4, ...) with the least estimated time,
+// rounds of programs over the CUs times a program's time (a fixed part and one per 32-row
+// subtile) plus, for nS > 1, the summing launch and the partials' traffic (written, then read).
+// FMLP_DW256_NS (read once per process) forces nS where its workspace fits.
+Dw256Plan plan_dw256(int64_t H, int64_t B, int64_t E, bool hilo, int num_cus, size_t max_ws) {
+  constexpr double kFixedUs = 4.0, kSubUs = 1.0, kSubHiloUs = 1.4;
+  static const int ns_env = env_int("FMLP_DW256_NS", 0);
+  Dw256Plan p{};
+  p.nE = (int)((E + DW_ET - 1) / DW_ET);
+  p.nS = 1;
+  p.rows_per_split = (int)rows_for_split(B, 1);
+  p.n = H * p.nE;
+  p.ws_bytes = 0;
+  if (p.n <= 0 || B <= 0) return p;
+  const long long N = num_cus > 0 ? num_cus : 1;
+  const long long max_ns = B / 256 > 1 ? B / 256 : 1;
+  const double t_sub = hilo ? kSubHiloUs : kSubUs;
+  double best = 1e300;
+  for (long long ns = 1; ns <= max_ns; ns *= 2) {
+    const long long rps = rows_for_split(B, ns), eff = (B + rps - 1) / rps;
+    const size_t ws = eff > 1 ? (size_t)2 * eff * H * E * 256 * sizeof(float) : 0;
+    if (ws > max_ws) continue;
+    const long long progs = H * p.nE * eff, rounds = (progs + N - 1) / N;
+    double cost = (double)rounds * (kFixedUs + (double)(rps / DW_BT) * t_sub);
+    if (eff > 1) cost += kPlanLaunchUs + 2.0 * (double)ws / kPlanHbmBytesPerUs;
+    // with the override: the first split that fits, replaced by the forced one
+    const bool take = ns_env > 0 ? (eff == ns_env || best == 1e300) : cost < best;
+    if (take) {
+      best = cost;
+      p.nS = (int)eff;
+      p.rows_per_split = (int)rps;
+      p.n = progs;
+      p.ws_bytes = ws;
+    }
+  }
+  return p;
+}
+
 // dynamic LDS of the dW role: a 3-group ring of subtiles and the two weight tiles
 template <int D, int ET>
 constexpr size_t dw_lds_bytes() {
   return 3u * 2u * (DW2_NW / (ET / 32)) * 64u * D + 2u * 2u * ET * D;
+}
+
+// sum of the dW programs' fp32 partials when B is split (nS > 1)
+template <bool BF16>
+static hipError_t launch_dw_reduce(const BwdArgs& a, int nS, hipStream_t st) {
+  if (nS <= 1) return hipSuccess;
+  const size_t items = 2 * ((size_t)a.H * a.E * a.D / 4);
+  size_t blocks = (items + 255) / 256;
+  if (blocks > 8192) blocks = 8192;
+  hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws, a.dw1, a.dw2,
+                     (int)a.H, (int)a.E, (int)a.D, nS, a.out_f32 ? 1 : 0);
+  return hipGetLastError();
 }
 
 template <bool BF16, int D, int ACT, int DES, int ET>
@@ -1312,15 +1615,7 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   // dX role's rings (one or two parts of DX_NSLOT slots of 128 D bytes)
   constexpr size_t lds = std::max<size_t>(dw_lds_bytes<D, ET>(), (size_t)DES * DX_NSLOT * 128u * D);
   static_assert(dw_lds_bytes<D, DW_ET>() == 1280u * D, "the 128-column form's LDS");
-  auto reduce = [&]() {          // sum of the dW programs' fp32 partials when B is split
-    if (p.nS <= 1) return hipSuccess;
-    const size_t items = 2 * ((size_t)a.H * a.E * a.D / 4);
-    size_t blocks = (items + 255) / 256;
-    if (blocks > 8192) blocks = 8192;
-    hipLaunchKernelGGL(dw_reduce_kernel<BF16>, dim3((unsigned)blocks), dim3(256), 0, st, (const float*)a.ws, a.dw1,
-                       a.dw2, (int)a.H, (int)a.E, (int)a.D, p.nS, a.out_f32 ? 1 : 0);
-    return hipGetLastError();
-  };
+  auto reduce = [&]() { return launch_dw_reduce<BF16>(a, p.nS, st); };
   if (p.dz && a.want_dx && a.want_dw) {  // stored-dZ form: dW programs storing dZ, their reduction, then the dX GEMM
     u16* dzt = (u16*)((char*)a.ws + p.dz_off);
     const int Ep = p.nE * DW_ET;
@@ -1444,6 +1739,37 @@ static hipError_t launch_dx256_a(const BwdArgs& a, hipStream_t st) {
 
 hipError_t launch_dx256(const BwdArgs& a, hipStream_t st) {
   return a.bf16 ? launch_dx256_a<true>(a, st) : launch_dx256_a<false>(a, st);
+}
+
+template <bool BF16, int ACT, bool HILO>
+static hipError_t launch_dw256_t(const BwdArgs& a, const Dw256Plan& p, hipStream_t st) {
+  if (p.n <= 0) return hipSuccess;
+  if (p.n > 0x7fffffffLL) return hipErrorInvalidValue;
+  constexpr size_t lds = (size_t)DW4_NSLOT * DW4_SLOT;
+  auto k = dw256_kernel<BF16, ACT, HILO>;
+  static std::atomic<unsigned long long> lds_set{0};
+  hipError_t e = set_lds_once((const void*)k, (int)lds, lds_set);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k, dim3((unsigned)p.n), dim3(256), lds, st, (const u16*)a.x, (const u16*)a.w1, (const u16*)a.w2,
+                     (const u16*)a.dout, a.dw1, a.dw2, (float*)a.ws, (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS,
+                     p.rows_per_split, a.out_f32 ? 1 : 0);
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  return launch_dw_reduce<BF16>(a, p.nS, st);
+}
+
+template <bool BF16, bool HILO>
+static hipError_t launch_dw256_a(const BwdArgs& a, const Dw256Plan& p, hipStream_t st) {
+  switch (a.act) {
+    case ACT_SILU: return launch_dw256_t<BF16, ACT_SILU, HILO>(a, p, st);
+    case ACT_LEAKY: return launch_dw256_t<BF16, ACT_LEAKY, HILO>(a, p, st);
+    case ACT_SIGMOID: return launch_dw256_t<BF16, ACT_SIGMOID, HILO>(a, p, st);
+    default: return launch_dw256_t<BF16, ACT_NONE, HILO>(a, p, st);
+  }
+}
+
+hipError_t launch_dw256(const BwdArgs& a, const Dw256Plan& p, hipStream_t st) {
+  if (a.bf16) return a.dw_hilo ? launch_dw256_a<true, true>(a, p, st) : launch_dw256_a<true, false>(a, p, st);
+  return a.dw_hilo ? launch_dw256_a<false, true>(a, p, st) : launch_dw256_a<false, false>(a, p, st);
 }
 
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st) {

@@ -147,9 +147,18 @@ hipError_t launch_fwd(const FwdArgs& a, hipStream_t st);
 hipError_t launch_tile_reduce(const float* ws, void* out, bool bf16, int B, int D, int BB, int H, int T, int xs,
                               int n_split, int outf32, hipStream_t st);
 hipError_t launch_bwd(const BwdArgs& a, const BwdPlan& p, hipStream_t st);
-// dX alone at D = 256 (dense 16-bit, E % 8 == 0): the tuned dX programs; the caller runs dW on
-// the generic kernels
+// dX alone at D = 256 (dense 16-bit, E % 8 == 0): the tuned dX programs
 hipError_t launch_dx256(const BwdArgs& a, hipStream_t st);
+// dW alone at D = 256 (dense 16-bit, E % 8 == 0): n = H nE nS programs (nE E-tiles of 128
+// columns, nS B ranges of rows_per_split rows), whose fp32 partials take ws_bytes of workspace
+// when nS > 1 (a split needing more than max_ws bytes is not taken)
+struct Dw256Plan {
+  int nE, nS, rows_per_split;
+  long long n;
+  size_t ws_bytes;
+};
+Dw256Plan plan_dw256(int64_t H, int64_t B, int64_t E, bool hilo, int num_cus, size_t max_ws);
+hipError_t launch_dw256(const BwdArgs& a, const Dw256Plan& p, hipStream_t st);
 
 // The library's static device scratch (fmlp_bwd_noalloc): its device address on the current
 // device, looked up once per device, and its size in bytes.

@@ -12,7 +12,8 @@
  * x's, flashmlp.py:87). All pointers are device pointers on the current HIP device, aligned
  * to their element size. Two kernel sets sit behind the entry points: the tuned gfx950
  * kernels for 16-bit io, D in {64, 128}, E % 8 == 0 on dense 16-byte aligned tensors
- * (fmlp_shape_tuned), and generic kernels for every other supported shape, dtype and layout.
+ * (fmlp_shape_tuned; with D = 256 kernels of their own for the same io, E and layout), and
+ * generic kernels for every other supported shape, dtype and layout.
  * The library never allocates: the caller passes every buffer, including the backward
  * workspace.
  *
@@ -111,8 +112,9 @@ int fmlp_shape_supported(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
 /* 1 when the tuned kernels take these shapes (16-bit io, D in {64, 128}, E % 8 == 0) on dense,
  * 16-byte aligned tensors; other supported shapes, dtypes and layouts run on the generic
- * kernels, except that the tuned forward also takes D = 256 (16-bit io, E % 8 == 0, dense,
- * aligned; its backward is generic). No counterpart in the reference (its Triton kernels are
+ * kernels, except that D = 256 (16-bit io, E % 8 == 0, dense, aligned) also has kernels of
+ * its own: the tuned forward and the backward's D = 256 dX and dW programs, which keep the
+ * generic kernels' workspace rule. No counterpart in the reference (its Triton kernels are
  * autotuned per shape). */
 int fmlp_shape_tuned(int64_t D, int64_t E, int dtype);
 
@@ -152,7 +154,8 @@ int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int
  * can change it (FMLP_DW_HILO, FMLP_BWD_RECOMPUTE, FMLP_BWD_STORE_DZ and FMLP_BWD_NO_DX change
  * the plan; with FMLP_BWD_NO_DW it is 0): query it with the flags of the call it is for. For
  * shapes the tuned kernels do not take, it is the fp32 partials of the generic dW programs'
- * B split; those calls (and fmlp_bwd_strided calls whose views send a tuned shape to the
+ * B split (16-bit D = 256 with E % 8 == 0: the larger of that and the D = 256 dW programs'
+ * split); those calls (and fmlp_bwd_strided calls whose views send a tuned shape to the
  * generic kernels) accept any workspace, NULL included, and split B only as far as it fits. */
 size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
@@ -166,9 +169,11 @@ int fmlp_bwd_stores_dz(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, in
  * (0/1), B splits of the dW programs, dX programs' in-workgroup E parts, parts of each split
  * ragged dX tile (0: not split), dX programs first (0/1), dW programs, whole-tile dX programs,
  * split-tile dX programs, workspace bytes, the activation's code, and the E-columns per dW
- * program (128 or 64). Returns FMLP_OK, or
- * FMLP_ERR_UNSUPPORTED for shapes the tuned kernels do not take. No counterpart in the
- * reference: a diagnostic for tests and benches. */
+ * program (128 or 64). Also for dense 16-bit D = 256 with E % 8 == 0 (the D = 256 dX and dW
+ * programs, one launch each; the split as with an unlimited workspace, which such calls take
+ * only as far as their workspace holds). Returns FMLP_OK, or FMLP_ERR_UNSUPPORTED for shapes
+ * the generic kernels take. No counterpart in the reference: a diagnostic for tests and
+ * benches. */
 int fmlp_bwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act, int64_t* info, int n_info);
 
 /*

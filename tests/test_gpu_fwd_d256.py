@@ -1,6 +1,6 @@
 """The tuned kernels at D = 256: the forward (fwd_kernel with four waves of 32 rows, one per SIMD)
 and the backward's dX programs (dx256_kernel, the same layout), for dense 16-bit tensors with
-E % 8 == 0; the backward's dW runs on the generic kernels there.
+E % 8 == 0 (the backward's dW programs there, dw256_kernel, have tests of their own).
 
 Each case checks through the C ABI:
   * the fp32 sums (FMLP_OUT_F32) against the oracle's cast-point emulation at the north star's
@@ -8,9 +8,9 @@ Each case checks through the C ABI:
     (so the generic path takes them) within 1e-5 (summation order only);
   * the io output against the fp32 autograd oracle at the parity bar (3e-2 + 3e-2 |ref|),
     every element written (output NaN-filled first);
-  * for the backward, dX's fp32 sums against the emulation and the generic kernel likewise, dW
-    bitwise equal to the all-generic backward's, and the partial backwards (FMLP_BWD_NO_DW,
-    FMLP_BWD_NO_DX) bitwise equal to the full one.
+  * for the backward, the fp32 sums of dX, dW1, dW2 against the emulation and the generic
+    kernels likewise, and the partial backwards (FMLP_BWD_NO_DW, FMLP_BWD_NO_DX) bitwise equal
+    to the full one.
 """
 import ctypes
 import sys
@@ -152,12 +152,10 @@ def test_tuned_dx_d256(dt, act, H, B, E):
     sg = _bwd(xv, w1d, w2d, dod, act, code | _lib.FMLP_OUT_F32, torch.float32)
     e = emulate.emu_bwd(x, w1, w2, do, act, dt, round_out=False)
     rel = {k: _normrel(g.cpu(), r) for k, g, r in zip(("dx", "dw1", "dw2"), s, e)}
-    rel_g = _normrel(s[0], sg[0])
+    rel_g = [_normrel(a_, b_) for a_, b_ in zip(s, sg)]
     sums = " ".join(f"{k}={v:.3g}" for k, v in rel.items())
-    _say(f"[bwd-d256] fp32 sums rel {sums}, dx to generic {rel_g:.3g}")
-    assert max(rel.values()) <= 1e-4 and rel_g <= 1e-5
-    for a_, b_ in zip(s[1:], sg[1:]):  # dW: the same generic kernels either way
-        assert torch.equal(a_, b_)
+    _say(f"[bwd-d256] fp32 sums rel {sums}, dx/dw1/dw2 to generic {['%.3g' % r for r in rel_g]}")
+    assert max(rel.values()) <= 1e-4 and max(rel_g) <= 1e-5
 
     dx, dw1, dw2 = _bwd(xd, w1d, w2d, dod, act, code, dt)
     _, rdx, _, _ = reference.autograd_grads(x, w1, w2, do, act)
