@@ -5,8 +5,8 @@
 // point, flashmlp.py:137-150) and O to the io dtype at the store (flashmlp.py:157).
 // The (H, B, E) intermediate never leaves registers.
 //
-// Per workgroup: D/16 waves (two per SIMD), each owning one 32-row M-tile (256 rows per
-// workgroup at D = 128, 128 at D = 64).
+// Per workgroup: D/16 waves, each owning one 32-row M-tile (256 rows per workgroup at
+// D = 128, 128 at D = 64); two waves per SIMD at D = 128, three at D = 64 (below).
 //   * X rows live in registers for the whole kernel, already in the MFMA B-operand layout
 //     of Z^T = W1c^T X^T (lane = row b, 8 consecutive d).
 //   * E is walked in 32-column chunks. Chunk k's W1c (D x 32) and W2c (32 x D) tiles are
@@ -61,16 +61,26 @@ __device__ __forceinline__ TileId main_tile(int m, int n_split, int H, int T) {
 // 4 D pieces of W1c and of W2c once); 4 at D = 256 (one wave per SIMD, whose O accumulators alone
 // take 128 registers; each thread loads 4 pieces per region).
 __host__ __device__ constexpr int fwd_waves(int D) { return D <= 128 ? D / 16 : 4; }
-__host__ __device__ constexpr int fwd_wpe(int D) { return D <= 128 ? 2 : 1; }  // waves per SIMD
+// OC: waves per SIMD the kernel is built for. Two up to D = 128 (each workgroup with an 8-slot
+// ring); at D = 64 without the E split three, each workgroup then with a 4-slot ring (32 KB) so
+// that three fit on a CU: the D = 64 kernel is VALU-issue bound (two activation elements per
+// MFMA) and a third wave per SIMD hides more of its latencies (measured on MI355X at H=8
+// B=65536 D=64 E=2048, fp16 sigmoid: forward 360 -> 343 us; a 6-slot ring spills registers
+// there and four waves per SIMD do not fit in 128 registers without spills); one at D = 256.
+__host__ __device__ constexpr int fwd_wpe(int D, int OC) { return D <= 128 ? OC : 1; }
 // ring geometry: slots (chunks of 128 D bytes), chunk iterations per workgroup barrier and chunks
-// loaded ahead; at D = 256 a chunk is 32 KB, so four slots, a barrier per chunk, two ahead
+// loaded ahead; at D = 256 a chunk is 32 KB, so four slots, a barrier per chunk, two ahead, and
+// the same for the 4-slot rings of the higher-occupancy D = 64 builds
 constexpr int FWD_PF = 4;  // chunks loaded ahead with one barrier per chunk (D <= 128)
-__host__ __device__ constexpr int fwd_nslot(int D) { return D <= 128 ? 8 : 4; }
-__host__ __device__ constexpr int fwd_sb(int D) { return D <= 128 ? 2 : 1; }
-__host__ __device__ constexpr int fwd_pf(int D) { return D <= 128 ? FWD_PF + fwd_sb(D) - 1 : 2; }
+__host__ __device__ constexpr bool fwd_small_ring(int D, int OC) { return D > 128 || OC > 2; }
+__host__ __device__ constexpr int fwd_nslot(int D, int OC) { return fwd_small_ring(D, OC) ? 4 : 8; }
+__host__ __device__ constexpr int fwd_sb(int D, int OC) { return fwd_small_ring(D, OC) ? 1 : 2; }
+__host__ __device__ constexpr int fwd_pf(int D, int OC) {
+  return fwd_small_ring(D, OC) ? fwd_nslot(D, OC) - 2 : FWD_PF + fwd_sb(D, OC) - 1;
+}
 
-template <bool BF16, int D, int ACT, int ES>
-__global__ void __launch_bounds__(fwd_waves(D) * ES * 64) __attribute__((amdgpu_waves_per_eu(fwd_wpe(D), fwd_wpe(D))))
+template <bool BF16, int D, int ACT, int ES, int OC = 2>
+__global__ void __launch_bounds__(fwd_waves(D) * ES * 64) __attribute__((amdgpu_waves_per_eu(fwd_wpe(D, OC), fwd_wpe(D, OC))))
 fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            void* __restrict__ O, int B, int E, int H, int tiles_per_head, int outf32, int n_main, int n_split,
            int xs, int nct, float* __restrict__ ws) {
@@ -84,11 +94,13 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   // SB: chunk iterations per workgroup barrier. The loads run SB - 1 chunks further ahead so
   // that a barrier covers the SB chunks read after it (measured on MI355X at cfg4: SB = 2 is
   // about 1 % faster than a barrier per chunk).
-  constexpr int SB = fwd_sb(D);
-  constexpr int NSLOT = fwd_nslot(D), PF = fwd_pf(D);
+  static_assert(OC == 2 || (D == 64 && ES == 1 && OC == 3), "occupancy");
+  constexpr int SB = fwd_sb(D, OC);
+  constexpr int NSLOT = fwd_nslot(D, OC), PF = fwd_pf(D, OC);
   constexpr int NPR = 4 * D / NT;  // 16-byte pieces per thread per region (W1c or W2c) of a chunk
   static_assert(SB == 1 || SB == 2, "barrier spacing");
   static_assert(PF >= 2 && PF <= NSLOT - 2 - (SB - 1) && (NSLOT & (NSLOT - 1)) == 0, "ring");
+  auto rslot = [](int c) -> unsigned { return (unsigned)(c & (NSLOT - 1)); };  // ring slot of chunk c
 
   const int lane = threadIdx.x & 63;
   const int part = ES == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x / NT);  // E part
@@ -145,7 +157,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     const int rem = D * E * 2 - 64 * cg;
     const i32x4 r1 = make_rsrc_words(W1h + (size_t)cg * 32, rem > 0 ? rem : 0);
     const i32x4 r2 = make_rsrc_words(W2h + (size_t)cg * 32 * D, clamp0(lim, 32) * D * 2);
-    const int slot = (int)RB + (c & (NSLOT - 1)) * (int)SLOT + wave * 1024;
+    const int slot = (int)RB + (int)rslot(c) * (int)SLOT + wave * 1024;
 #pragma unroll
     for (int k = 0; k < NPR; ++k) {
       buf_load16_lds(r1, colq[k] < lim ? dOffW1[k] : BUF_OOB, slot + k * NT * 16);
@@ -222,7 +234,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     constexpr int N1 = DO_G1 ? KS : 0, N2 = DO_G2 ? KS : 0, NOPS = N1 + N2;
     // activation elements of step j: [16 j / NOPS, 16 (j + 1) / NOPS) (one or two per step at
     // D <= 128, one every other step at D = 256)
-    const unsigned base1 = RB + ((c + 1) & (NSLOT - 1)) * SLOT, base2 = RB + ((c - 1) & (NSLOT - 1)) * SLOT;
+    const unsigned base1 = RB + rslot(c + 1) * SLOT, base2 = RB + rslot(c - 1) * SLOT;
 
     // chunk c+PF is requested straight into its LDS slot (PF chunks ahead of the one read)
     dma_chunk(c + PF);
@@ -265,7 +277,7 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
     if constexpr (decltype(SYNC)::value) chunk_end();
   };
   auto last_gemm2 = [&](const St& st) {
-    const unsigned base2 = RB + ((NC - 1) & (NSLOT - 1)) * SLOT;
+    const unsigned base2 = RB + rslot(NC - 1) * SLOT;
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
@@ -435,10 +447,10 @@ FwdPlan fwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t
   return p;
 }
 
-template <bool BF16, int D, int ACT, int ES>
+template <bool BF16, int D, int ACT, int ES, int OC = 2>
 static hipError_t launch_fwd_e(const FwdArgs& a, const FwdPlan& p, int tiles_per_head, hipStream_t st) {
-  const size_t lds = (size_t)ES * fwd_nslot(D) * 128u * D;
-  auto k = fwd_kernel<BF16, D, ACT, ES>;
+  const size_t lds = (size_t)ES * fwd_nslot(D, OC) * 128u * D;
+  auto k = fwd_kernel<BF16, D, ACT, ES, OC>;
   static std::atomic<unsigned long long> lds_set{0};
   hipError_t e = set_lds_once((const void*)k, (int)lds, lds_set);
   if (e != hipSuccess) return e;
@@ -476,6 +488,9 @@ static hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t st) {
   const FwdPlan p = fwd_plan(a.H, a.B, D, a.E, a.num_cus, a.ws != nullptr ? a.ws_bytes : 0);
   if constexpr (D == 64) {
     if (p.es == 2) return launch_fwd_e<BF16, D, ACT, 2>(a, p, tiles_per_head, st);
+    // FMLP_FWD_OCC=2 (read once per process) keeps two waves per SIMD
+    static const int occ = env_int("FMLP_FWD_OCC", 3);
+    if (occ != 2) return launch_fwd_e<BF16, D, ACT, 1, 3>(a, p, tiles_per_head, st);
   }
   return launch_fwd_e<BF16, D, ACT, 1>(a, p, tiles_per_head, st);
 }
