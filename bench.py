@@ -23,7 +23,7 @@ The default (cfg4) line also carries, measured in the same process after the hea
   * `configs`: every other BASELINE.json configuration (cfg2, cfg3, cfg5 sigmoid and linear,
     the forward-only cfg5s sweep) on the tuned kernels, and two shapes outside the tuned
     kernels' main range: the reference's CPU configuration cfg1 in fp32 (generic kernels) and
-    D = 256 (tuned forward and dX programs, generic dW programs);
+    D = 256 (its own tuned forward, dX and dW programs);
   * `vs_pytorch_unfused`: the unfused PyTorch path (bmm -> activation -> bmm, the (H, B, E)
     intermediates kept, manual backward) on the same GPU against FlashMLP, at cfg4 and at the
     four shapes of the reference's performance.md (example.py:98-135 compares the two);
@@ -68,7 +68,7 @@ WORKLOADS = {
     "cfg5_linear": (8, 4097, 64, 2048, "f16", "", 2.0, False),
     "cfg5s": (8, 65536, 64, 2048, "f16", "sigmoid", 2.0, True),
     # the reference's CPU configuration in fp32 (generic kernels), and
-    # D = 256 (tuned forward and dX programs, generic dW programs)
+    # D = 256 (its own tuned forward, dX and dW programs)
     "cfg1_fp32": (12, 1024, 64, 768, "f32", "silu", 1.0, False),
     "d256": (8, 4096, 256, 1024, "bf16", "silu", 1.0, False),
 }
