@@ -26,8 +26,8 @@ Differences from the reference, all deliberate:
   * Leaky ReLU's derivative at Z == 0 is autograd's 0.01 (flashmlp.py:33-34 uses 1.0);
   * io dtypes are fp16, bf16 and fp32 (fp32 in true fp32, where the reference's tl.dot would
     use its default reduced input precision); other dtypes raise TypeError;
-  * strided inputs are accepted: shapes the tuned kernels take (16-bit io, D in {64, 128},
-    E % 8 == 0) copy them to dense tensors, as the reference's reshape / contiguous does
+  * strided inputs are accepted: shapes with kernels of their own (16-bit io, D in {64, 128,
+    256}, E % 8 == 0) copy them to dense tensors, as the reference's reshape / contiguous does
     (flashmlp.py:453-459,508); every other shape reads the views in place (generic kernels),
     where the reference would copy them or fail its contiguity assertions.
 """
@@ -101,8 +101,13 @@ def _alloc_ws(nbytes: int, device: torch.device):
 
 
 @functools.lru_cache(maxsize=1024)
-def _tuned(D: int, E: int, dtype: int) -> bool:
-    return bool(_lib.lib().fmlp_shape_tuned(D, E, dtype))
+def _own_kernels(D: int, E: int, dtype: int) -> bool:
+    # shapes with kernels of their own, which take dense 16-byte aligned tensors: the tuned
+    # kernels (fmlp_shape_tuned) and the D = 256 programs (16-bit io, E % 8 == 0); views of
+    # other shapes go to the generic kernels in place
+    if _lib.lib().fmlp_shape_tuned(D, E, dtype):
+        return True
+    return D == 256 and E % 8 == 0 and dtype in (_lib.FMLP_DTYPE_F16, _lib.FMLP_DTYPE_BF16)
 
 
 # torch's current HIP stream of a device, as the raw handle the C ABI takes, and the current
@@ -177,7 +182,7 @@ def flashmlp_fwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, activation
         torch.cuda.set_device(dev)
     try:
         stream = _stream_of(dev)
-        if _tuned(D, E, dtype):
+        if _own_kernels(D, E, dtype):
             x, w1, w2 = _dense_all(x, w1, w2)
             ws_bytes = _fwd_ws_bytes(dev, H, B, D, E, dtype)
             try:
@@ -246,7 +251,7 @@ def flashmlp_bwd(x: torch.Tensor, w1: torch.Tensor, w2: torch.Tensor, do: torch.
         torch.cuda.set_device(dev)
     try:
         stream = _stream_of(dev)
-        if _tuned(D, E, dtype):
+        if _own_kernels(D, E, dtype):
             x, w1, w2, do = _dense_all(x, w1, w2, do)
             ws_bytes = _ws_bytes(dev, H, B, D, E, flags)
             try:

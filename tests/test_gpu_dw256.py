@@ -190,3 +190,28 @@ def test_dw256_few_rows():
     _, dw1, dw2 = _bwd(x, w1, w2, do, "silu", _DT[torch.float16], torch.float16)
     assert torch.count_nonzero(dw1.float().nan_to_num(1.0)) == 0
     assert torch.count_nonzero(dw2.float().nan_to_num(1.0)) == 0
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_d256_views_take_the_d256_programs(dt):
+    """Through the Python API, views at D = 256 (X transposed from a (B, H, D) tensor, and the
+    stride-0 dO that `model(x).sum().backward()` hands to the backward) are copied to dense
+    tensors, as the reference's reshape / contiguous does (flashmlp.py:453-459,508), and run on
+    the D = 256 programs: outputs bitwise equal to the same values passed densely (the generic
+    kernels, which read views in place, sum in another order)."""
+    import flashmlp_amd as fm
+
+    H, B, E, act = 3, 1000, 264, "silu"
+    x, w1, w2, _ = make_inputs(H, B, D, E, dt, 1.0, seed=65)
+    xd, w1d, w2d = (t.cuda() for t in (x, w1, w2))
+    xv = xd.transpose(0, 1).contiguous().transpose(0, 1)  # same values, strides (D, H D, 1)
+    assert not xv.is_contiguous()
+    one = torch.ones((), dtype=dt, device="cuda")
+    dov, dod = one.expand(H, B, D), one.expand(H, B, D).contiguous()
+    _say(f"[dw256] views through the Python API: H={H} B={B} E={E} {dt}")
+    o_v, o_d = fm.flashmlp_fwd(xv, w1d, w2d, act), fm.flashmlp_fwd(xd, w1d, w2d, act)
+    g_v, g_d = fm.flashmlp_bwd(xv, w1d, w2d, dov, act), fm.flashmlp_bwd(xd, w1d, w2d, dod, act)
+    torch.cuda.synchronize()
+    for name, a, b in zip(("o", "dx", "dw1", "dw2"), (o_v, *g_v), (o_d, *g_d)):
+        assert torch.isfinite(b).all(), name
+        assert torch.equal(a, b), f"{name}: the view's result differs from the dense call's"
