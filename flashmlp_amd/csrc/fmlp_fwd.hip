@@ -34,7 +34,9 @@ namespace fmlp {
 // ES = 2 (E split, D = 64 only, for grids that leave CUs idle): the workgroup holds two such
 // sets of waves on the same rows, each walking half of the E-chunks through a ring of its own
 // (one workgroup per CU, two waves per SIMD instead of one); the two partial O tiles are added
-// through LDS at the end.
+// through LDS at the end. ES = 4 with NWP = 2 (D = 64, smaller grids still): 64-row tiles, four
+// sets of two waves, each walking a quarter of the E-chunks through a 4-slot ring of its own;
+// the partial tiles are added in part order.
 // Split tiles (fwd_plan): the last n_split tiles in row-block-major order (tile (h, bt) at
 // bt H + h; the ragged last tiles of the heads first) are split; the first n_main workgroups
 // each own one of the other tiles, enumerated head by head (split_tile / main_tile); every later
@@ -72,31 +74,32 @@ __host__ __device__ constexpr int fwd_wpe(int D, int OC) { return D <= 128 ? OC 
 // loaded ahead; at D = 256 a chunk is 32 KB, so four slots, a barrier per chunk, two ahead, and
 // the same for the 4-slot rings of the higher-occupancy D = 64 builds
 constexpr int FWD_PF = 4;  // chunks loaded ahead with one barrier per chunk (D <= 128)
-__host__ __device__ constexpr bool fwd_small_ring(int D, int OC) { return D > 128 || OC > 2; }
-__host__ __device__ constexpr int fwd_nslot(int D, int OC) { return fwd_small_ring(D, OC) ? 4 : 8; }
-__host__ __device__ constexpr int fwd_sb(int D, int OC) { return fwd_small_ring(D, OC) ? 1 : 2; }
-__host__ __device__ constexpr int fwd_pf(int D, int OC) {
-  return fwd_small_ring(D, OC) ? fwd_nslot(D, OC) - 2 : FWD_PF + fwd_sb(D, OC) - 1;
+__host__ __device__ constexpr bool fwd_small_ring(int D, int OC, int ES = 1) { return D > 128 || OC > 2 || ES > 2; }
+__host__ __device__ constexpr int fwd_nslot(int D, int OC, int ES = 1) { return fwd_small_ring(D, OC, ES) ? 4 : 8; }
+__host__ __device__ constexpr int fwd_sb(int D, int OC, int ES = 1) { return fwd_small_ring(D, OC, ES) ? 1 : 2; }
+__host__ __device__ constexpr int fwd_pf(int D, int OC, int ES = 1) {
+  return fwd_small_ring(D, OC, ES) ? fwd_nslot(D, OC, ES) - 2 : FWD_PF + fwd_sb(D, OC, ES) - 1;
 }
 
-template <bool BF16, int D, int ACT, int ES, int OC = 2>
-__global__ void __launch_bounds__(fwd_waves(D) * ES * 64) __attribute__((amdgpu_waves_per_eu(fwd_wpe(D, OC), fwd_wpe(D, OC))))
+template <bool BF16, int D, int ACT, int ES, int OC = 2, int NWP = fwd_waves(D)>
+__global__ void __launch_bounds__(NWP * ES * 64) __attribute__((amdgpu_waves_per_eu(fwd_wpe(D, OC), fwd_wpe(D, OC))))
 fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __restrict__ W2,
            void* __restrict__ O, int B, int E, int H, int tiles_per_head, int outf32, int n_main, int n_split,
            int xs, int nct, float* __restrict__ ws) {
-  constexpr int NW = fwd_waves(D), NT = NW * 64;  // waves, threads of one E part
+  constexpr int NW = NWP, NT = NW * 64;  // waves, threads of one E part
   constexpr int KS = D / 16;           // K steps of GEMM1 (= GEMM2 operand count 2 * D/32)
   constexpr int NTN = D / 32;          // N tiles of GEMM2
   constexpr int BB = NW * 32;          // rows per workgroup (32 per wave)
-  static_assert(ES == 1 || (ES == 2 && D == 64), "E split");
+  static_assert(ES == 1 || (ES == 2 && D == 64) || (ES == 4 && D == 64 && NWP == 2), "E split");
+  static_assert(NWP == fwd_waves(D) || (NWP == 2 && ES == 4), "waves per E part");
   constexpr unsigned SLOT = 128u * D;  // bytes per ring slot: W1c (64*D) + W2c (64*D)
   constexpr unsigned W2OFF = 64u * D;
   // SB: chunk iterations per workgroup barrier. The loads run SB - 1 chunks further ahead so
   // that a barrier covers the SB chunks read after it (measured on MI355X at cfg4: SB = 2 is
   // about 1 % faster than a barrier per chunk).
   static_assert(OC == 2 || (D == 64 && ES == 1 && OC == 3), "occupancy");
-  constexpr int SB = fwd_sb(D, OC);
-  constexpr int NSLOT = fwd_nslot(D, OC), PF = fwd_pf(D, OC);
+  constexpr int SB = fwd_sb(D, OC, ES);
+  constexpr int NSLOT = fwd_nslot(D, OC, ES), PF = fwd_pf(D, OC, ES);
   constexpr int NPR = 4 * D / NT;  // 16-byte pieces per thread per region (W1c or W2c) of a chunk
   static_assert(SB == 1 || SB == 2, "barrier spacing");
   static_assert(PF >= 2 && PF <= NSLOT - 2 - (SB - 1) && (NSLOT & (NSLOT - 1)) == 0, "ring");
@@ -314,11 +317,13 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
   }
 
   wait_vmcnt<0>();  // chunks past the last are still landing (as zeros)
-  if constexpr (ES == 2) {  // part 1 hands its partial O tile to part 0 through LDS (the rings)
+  if constexpr (ES > 1) {  // parts 1 .. ES-1 hand their partial O tiles to part 0 through LDS (the rings)
     asm volatile("" ::: "memory");
     __syncthreads();
-    const int ob = wave * (NTN * 4096);  // per wave NTN x 4 x [64 lanes][16 bytes]
-    if (part == 1) {
+    // per wave NTN x 4 x [64 lanes][16 bytes], one region per handing part
+    const int ob = wave * (NTN * 4096) + (part > 0 ? part - 1 : 0) * (NW * NTN * 4096);
+    static_assert((ES - 1) * NW * NTN * 4096 <= ES * NSLOT * (int)SLOT, "the partial tiles fit the rings");
+    if (part > 0) {
 #pragma unroll
       for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
@@ -328,15 +333,17 @@ fwd_kernel(const u16* __restrict__ X, const u16* __restrict__ W1, const u16* __r
                             __float_as_uint(o[nt][4 * i4 + 2]), __float_as_uint(o[nt][4 * i4 + 3])});
     }
     __syncthreads();
-    if (part == 1) return;
+    if (part > 0) return;
 #pragma unroll
-    for (int nt = 0; nt < NTN; ++nt)
+    for (int p = 1; p < ES; ++p)  // in part order
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const u32x4 v = lds_read16(ob + ((nt * 4 + i4) * 64 + lane) * 16);
+      for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[nt][4 * i4 + j] += __uint_as_float(v[j]);
-      }
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const u32x4 v = lds_read16(ob + (p - 1) * (NW * NTN * 4096) + ((nt * 4 + i4) * 64 + lane) * 16);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) o[nt][4 * i4 + j] += __uint_as_float(v[j]);
+        }
   }
   // ---- epilogue: O tile (C layout: lane = column d, rows 8(i/4) + 4g + i%4); fp32 sums
   // when the caller asked for them (FMLP_OUT_F32), else rounded to the io dtype; a split
@@ -418,6 +425,19 @@ FwdPlan fwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t
   p.n_main = R;
   p.xs = 1;
   p.nct = (int)nch;
+  // 64-row tiles in four E parts of two waves: twice the workgroups of the split above, each
+  // walking a quarter of the chunks, when they still fit on the CUs at one each and every part
+  // gets at least two chunks. These grids are latency-bound (one round, short chunk loops):
+  // measured on MI355X at H=12 B=1024 D=64 E=768 fp16, forward 11.6 -> 8.8 us, at H=8 B=512
+  // E=512 bf16 8.8 -> 6.9 us. FMLP_FWD_T64=0 (read once per process) keeps 128-row tiles.
+  static const int t64_env = env_int("FMLP_FWD_T64", 1);
+  const long long R64 = H * ((B + 63) / 64);
+  if (t64_env != 0 && p.es == 2 && force != 1 && R <= N && R64 <= N && nch >= 8) {
+    p.es = 4;
+    p.nwp = 2;
+    p.n_main = R64;
+    return p;
+  }
   if (xs_env == 0 || R <= 0) return p;
   long long cand = 0;
   int es = p.es;
@@ -447,19 +467,19 @@ FwdPlan fwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int num_cus, size_t
   return p;
 }
 
-template <bool BF16, int D, int ACT, int ES, int OC = 2>
+template <bool BF16, int D, int ACT, int ES, int OC = 2, int NWP = fwd_waves(D)>
 static hipError_t launch_fwd_e(const FwdArgs& a, const FwdPlan& p, int tiles_per_head, hipStream_t st) {
-  const size_t lds = (size_t)ES * fwd_nslot(D, OC) * 128u * D;
-  auto k = fwd_kernel<BF16, D, ACT, ES, OC>;
+  const size_t lds = (size_t)ES * fwd_nslot(D, OC, ES) * 128u * D;
+  auto k = fwd_kernel<BF16, D, ACT, ES, OC, NWP>;
   static std::atomic<unsigned long long> lds_set{0};
   hipError_t e = set_lds_once((const void*)k, (int)lds, lds_set);
   if (e != hipSuccess) return e;
   const long long grid = p.n_main + (long long)p.n_split * p.xs;
-  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(64 * ES * fwd_waves(D)), lds, st, (const u16*)a.x,
+  hipLaunchKernelGGL(k, dim3((unsigned)grid), dim3(64 * ES * NWP), lds, st, (const u16*)a.x,
                      (const u16*)a.w1, (const u16*)a.w2, a.o, (int)a.B, (int)a.E, (int)a.H, tiles_per_head,
                      a.out_f32 ? 1 : 0, (int)p.n_main, p.n_split, p.xs, p.nct, (float*)a.ws);
   if ((e = hipGetLastError()) != hipSuccess || p.n_split == 0) return e;
-  return launch_tile_reduce((const float*)a.ws, a.o, BF16, (int)a.B, D, 32 * fwd_waves(D), (int)a.H, tiles_per_head,
+  return launch_tile_reduce((const float*)a.ws, a.o, BF16, (int)a.B, D, 32 * NWP, (int)a.H, tiles_per_head,
                             p.xs, p.n_split, a.out_f32 ? 1 : 0, st);
 }
 
@@ -480,13 +500,14 @@ hipError_t launch_tile_reduce(const float* ws, void* out, bool bf16, int B, int 
 
 template <bool BF16, int D, int ACT>
 static hipError_t launch_fwd_t(const FwdArgs& a, hipStream_t st) {
-  constexpr int BB = 32 * fwd_waves(D);
-  const int tiles_per_head = (int)((a.B + BB - 1) / BB);
-  const long long grid = (long long)tiles_per_head * a.H;
-  if (grid <= 0) return hipSuccess;
-  if (grid > 0x7fffffffLL) return hipErrorInvalidValue;
+  constexpr int BB0 = 32 * fwd_waves(D);
+  if ((a.B + BB0 - 1) / BB0 * a.H <= 0) return hipSuccess;
+  if ((a.B + 63) / 64 * a.H > 0x7fffffffLL) return hipErrorInvalidValue;
   const FwdPlan p = fwd_plan(a.H, a.B, D, a.E, a.num_cus, a.ws != nullptr ? a.ws_bytes : 0);
+  const int BB = 32 * (p.nwp > 0 ? p.nwp : fwd_waves(D));
+  const int tiles_per_head = (int)((a.B + BB - 1) / BB);
   if constexpr (D == 64) {
+    if (p.es == 4) return launch_fwd_e<BF16, D, ACT, 4, 2, 2>(a, p, tiles_per_head, st);
     if (p.es == 2) return launch_fwd_e<BF16, D, ACT, 2>(a, p, tiles_per_head, st);
     // FMLP_FWD_OCC=2 (read once per process) keeps two waves per SIMD
     static const int occ = env_int("FMLP_FWD_OCC", 3);

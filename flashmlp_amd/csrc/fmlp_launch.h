@@ -30,12 +30,14 @@ struct FwdArgs {
   size_t ws_bytes = 0;
 };
 
-// Forward work split (fwd_plan): es = E parts inside a workgroup (1, or 2 at D = 64); tiles
+// Forward work split (fwd_plan): es = E parts inside a workgroup (1, or 2 or 4 at D = 64, 4 with
+// nwp = 2 waves per part and 64-row tiles); tiles
 // 0 .. n_main - 1 run whole, the last n_split tiles each as xs workgroups of nct E-chunks whose
 // fp32 partials take ws_bytes of workspace (0 and n_split = 0 when nothing is split). A split
 // needing more than max_ws bytes is not taken.
 struct FwdPlan {
   int es;
+  int nwp = 0;  // waves per E part (32 rows each): 0 = fwd_waves(D); 2 = 64-row tiles (D = 64, es = 4)
   long long n_main;
   int n_split, xs, nct;
   size_t ws_bytes;

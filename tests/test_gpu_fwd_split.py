@@ -141,3 +141,45 @@ def test_python_forward_uses_split():
     b = flashmlp_fwd(xd, w1d, w2d, act)
     torch.cuda.synchronize()
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+def _t64_cases():
+    n = _cus()
+    # (name, H, B, E, dtype, act): D = 64 grids whose 64-row tiles fit on the CUs at one workgroup
+    # each (H ceil(B / 64) <= CUs) with at least 8 E-chunks: the forward's 64-row tiles in four
+    # E parts of two waves
+    return [
+        ("cfg2", 12, 1024, 768, torch.float16, "silu"),
+        ("ragged-B-E-tail", 3, 1000, 264, torch.bfloat16, "sigmoid"),  # 9 chunks: the 4th part's are past E
+        ("tiny-B", 5, 129, 256, torch.float16, ""),
+        ("long-E", 2, 64, 2048, torch.bfloat16, "silu"),
+        ("full-round", n // 4, 256 - 17, 512, torch.bfloat16, "leaky_relu"),
+    ]
+
+
+@pytest.mark.parametrize("case", range(5), ids=[c[0] for c in _t64_cases()] if torch.cuda.is_available() else None)
+def test_forward_64_row_tiles(case):
+    """D = 64 grids small enough for 64-row tiles (fwd_plan: four E parts of two waves, each
+    through a 4-slot ring, partial tiles added in part order): fp32 sums against the emulation at
+    1e-4 with the output NaN-filled first, io output at the parity bar, bitwise repeats, and no
+    workspace (fmlp_fwd_workspace_bytes is 0)."""
+    name, H, B, E, dt, act = _t64_cases()[case]
+    D = 64
+    L = _lib.lib()
+    code = _DT[dt]
+    assert H * ((B + 63) // 64) <= _cus() and (E + 31) // 32 >= 8, "the case must take the 64-row tiles"
+    assert L.fmlp_fwd_workspace_bytes(H, B, D, E, code) == 0
+    _say(f"[fwd-t64] {name}: H={H} B={B} D={D} E={E} {dt} act='{act}'")
+    x, w1, w2, _ = make_inputs(H, B, D, E, dt, 1.0, seed=40 + case, with_do=False)
+    xd, w1d, w2d = (t.cuda() for t in (x, w1, w2))
+    s = _fwd(L, xd, w1d, w2d, act, code | _lib.FMLP_OUT_F32, torch.float32, fill_nan=True)
+    assert torch.isfinite(s).all()
+    rel = _normrel(s.cpu(), emulate.emu_fwd(x, w1, w2, act, dt, round_out=False))
+    o1 = _fwd(L, xd, w1d, w2d, act, code, dt, fill_nan=True)
+    o2 = _fwd(L, xd, w1d, w2d, act, code, dt)
+    ref = emulate.emu_fwd(x, w1, w2, act, dt, round_out=True).float()
+    bad = ((o1.float().cpu() - ref).abs() > 3e-2 + 3e-2 * ref.abs()).sum().item()
+    _say(f"[fwd-t64] {name}: fp32 sums rel to oracle {rel:.3g}, {bad} io elements outside 3e-2")
+    assert rel <= 1e-4
+    assert bad == 0
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
