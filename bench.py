@@ -28,7 +28,8 @@ The default (cfg4) line also carries, measured in the same process after the hea
     intermediates kept, manual backward) on the same GPU against FlashMLP, at cfg4 and at the
     four shapes of the reference's performance.md (example.py:98-135 compares the two);
   * `memory`: peak allocated MB of one fwd+bwd for both backward forms and the unfused path
-    (example.py:142-200), plus the device memory the library's code objects hold;
+    (example.py:142-200), plus the device memory the library's code objects hold, and
+    example.py's own module comparison at the five shapes of performance.md's memory table;
   * `autograd_ms_per_step` (FlashMLPFunction forward + backward, as example.py:120-128 times
     the module), host microseconds per call;
   * `cpu_baseline`: the CPU oracle (torch fp32 autograd of the restated reference path) on a
@@ -76,6 +77,15 @@ WORKLOADS = {
 CONFIG_PASS = ["cfg2", "cfg3", "cfg5", "cfg5_linear", "cfg5s", "cfg1_fp32", "d256"]
 # performance.md:9-12 (example.py:86-91): bf16, SiLU, timed through the FlashMLP module
 EXAMPLE_SHAPES = [(8, 512, 64, 512), (12, 1024, 64, 768), (16, 2048, 64, 1024), (32, 4096, 64, 512)]
+# performance.md:24-30 (example.py:142-200): peak and forward-allocated MB of one module forward +
+# backward, PyTorch vs the reference's FlashMLP, bf16 SiLU
+MEMORY_SHAPES = [(8, 512, 64, 512), (12, 1024, 64, 768), (16, 2048, 64, 1024), (32, 4096, 64, 512),
+                 (12, 4096, 64, 768)]
+MEMORY_PUBLISHED_MB = {  # (PyTorch peak, FlashMLP peak, PyTorch fwd, FlashMLP fwd)
+    (8, 512, 64, 512): (13.5, 2.5, 8.5, 0.5), (12, 1024, 64, 768): (58.1, 7.5, 37.5, 1.5),
+    (16, 2048, 64, 1024): (202.0, 16.0, 132.0, 4.0), (32, 4096, 64, 512): (418.0, 52.0, 272.0, 16.0),
+    (12, 4096, 64, 768): (229.1, 21.0, 150.0, 6.0),
+}
 EXAMPLE_PUBLISHED_MS = {  # (fwd, fwd+bwd) of the reference on its (unstated) hardware
     (8, 512, 64, 512): (0.036, 0.217), (12, 1024, 64, 768): (0.035, 0.222),
     (16, 2048, 64, 1024): (0.036, 0.219), (32, 4096, 64, 512): (0.060, 0.380),
@@ -219,6 +229,47 @@ def _device_used():
 
     free, total = torch.cuda.mem_get_info()
     return total - free
+
+
+def module_memory():
+    """example.py:142-200's comparison, as it runs it: per shape, a PyTorchMLP and a FlashMLP module
+    (bf16, SiLU), one warm-up forward + `.sum().backward()`, then peak allocated MB of one more
+    (max_memory_allocated minus the memory allocated before the forward) and the MB the forward
+    leaves allocated; the reference's published rows beside them (performance.md:24-30)."""
+    import numpy as np
+    import torch
+
+    import flashmlp_amd as fm
+
+    rows = []
+    for H, B, D, E in MEMORY_SHAPES:
+        r = {"H": H, "B": B, "D": D, "E": E}
+        for name, cls in (("pytorch", fm.PyTorchMLP), ("flashmlp", fm.FlashMLP)):
+            torch.cuda.empty_cache()
+            model = cls(H, D, E, activation="silu", dtype=torch.bfloat16, device="cuda")
+            xw = (torch.randn(H, B, D, device="cuda", dtype=torch.bfloat16) / np.sqrt(D)).requires_grad_(True)
+            model(xw).sum().backward()
+            del xw
+            model.zero_grad()
+            torch.cuda.empty_cache()
+            torch.cuda.reset_peak_memory_stats()
+            x = (torch.randn(H, B, D, device="cuda", dtype=torch.bfloat16) / np.sqrt(D)).requires_grad_(True)
+            before = torch.cuda.memory_allocated()
+            o = model(x)
+            fwd_mb = (torch.cuda.memory_allocated() - before) / 2 ** 20
+            o.sum().backward()
+            torch.cuda.synchronize()
+            r[f"{name}_peak_mb"] = round((torch.cuda.max_memory_allocated() - before) / 2 ** 20, 1)
+            r[f"{name}_fwd_mb"] = round(fwd_mb, 1)
+            del model, x, o
+            torch.cuda.empty_cache()
+        r["peak_savings"] = round(1 - r["flashmlp_peak_mb"] / r["pytorch_peak_mb"], 4)
+        r["fwd_savings"] = round(1 - r["flashmlp_fwd_mb"] / r["pytorch_fwd_mb"], 4)
+        pub = MEMORY_PUBLISHED_MB[(H, B, D, E)]
+        r["reference_published_mb"] = {"pytorch_peak": pub[0], "triton_peak": pub[1], "pytorch_fwd": pub[2],
+                                       "triton_fwd": pub[3]}
+        rows.append(r)
+    return rows
 
 
 def peak_memory(x, w1, w2, do, activation):
@@ -753,6 +804,8 @@ def main():
             line["vs_pytorch_unfused"] = vs_unfused(x, w1, w2, do, act, 10, 3)
     if not args.no_memory and not fwd_only:
         line["memory"] = peak_memory(x, w1, w2, do, act)
+        if args.workload == "cfg4" and not args.no_extra:
+            line["memory"]["performance_md_shapes"] = module_memory()
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(H, B, D, E, act, x_std)
     print(json.dumps(line), flush=True)
