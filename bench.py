@@ -23,7 +23,8 @@ The default (cfg4) line also carries, measured in the same process after the hea
   * `configs`: every other BASELINE.json configuration (cfg2, cfg3, cfg5 sigmoid and linear,
     the forward-only cfg5s sweep) on the tuned kernels, and two shapes outside the tuned
     kernels' main range: the reference's CPU configuration cfg1 in fp32 (generic kernels) and
-    D = 256 (its own tuned forward, dX and dW programs);
+    D = 256 (its own tuned forward, dX and dW programs); per configuration also its peak
+    memory against the unfused path and the CPU oracle's time per step;
   * `vs_pytorch_unfused`: the unfused PyTorch path (bmm -> activation -> bmm, the (H, B, E)
     intermediates kept, manual backward) on the same GPU against FlashMLP, at cfg4 and at the
     four shapes of the reference's performance.md (example.py:98-135 compares the two);
@@ -464,6 +465,48 @@ def _summary(H, B, D, E, dt_name, act, fwd_only, wall, fwd_ms, bwd_ms, bwd_form)
     return r
 
 
+def _peak_mb(run):
+    """Peak allocated MB of run() over the memory allocated before it (example.py:142-200's
+    method), after one unmeasured run."""
+    import torch
+
+    run()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch.cuda.reset_peak_memory_stats()
+    base = torch.cuda.memory_allocated()
+    out = run()
+    torch.cuda.synchronize()
+    peak = (torch.cuda.max_memory_allocated() - base) / 2 ** 20
+    del out
+    torch.cuda.empty_cache()
+    return round(peak, 1)
+
+
+def _cpu_config_ms(H, B, D, E, act, x_std, fwd_only):
+    """The CPU oracle (torch fp32 autograd of the restated reference path, the forward alone for
+    a forward-only workload) on one head of the workload, median of 3 after a warm-up, scaled to
+    all H heads (heads are independent): milliseconds per full step."""
+    import torch
+
+    from oracle import reference
+    from oracle.inputs import make_inputs
+
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    x, w1, w2, do = make_inputs(1, B, D, E, torch.float32, x_std, seed=0)
+    if fwd_only:
+        f = lambda: reference.torch_fwd(x, w1, w2, act)
+    else:
+        f = lambda: reference.autograd_grads(x, w1, w2, do, act)
+    f()
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        f()
+        ts.append(time.perf_counter() - t0)
+    return round(statistics.median(ts) * 1e3 * H, 2)
+
+
 def run_config(name, steps, warmup, **bwd_kw):
     """One workload's step timed on freshly drawn inputs (the `configs` pass)."""
     import torch
@@ -482,6 +525,40 @@ def run_config(name, steps, warmup, **bwd_kw):
         r["note"] = "forward only (inference sweep)"
     del x, w1, w2, do, outs
     torch.cuda.empty_cache()
+    return r
+
+
+def config_extras(name):
+    """A workload's peak allocated MB of one step against the unfused PyTorch path, and the CPU
+    oracle's time per step on the host's cores (one head, scaled to all). Run after every
+    configuration is timed: the oracle's host threads keep spinning for a while after it, which
+    would slow the launches of the next timed steps."""
+    import torch
+
+    import flashmlp_amd as fm
+
+    H, B, D, E, dt_name, act, x_std, fwd_only = WORKLOADS[name]
+    x, w1, w2, do = make_gpu_inputs(H, B, D, E, _torch_dtype(dt_name), x_std)
+    fwd = lambda: fm.flashmlp_fwd(x, w1, w2, act)
+    bwd = lambda: fm.flashmlp_bwd(x, w1, w2, do, act)
+    r = {}
+    if fwd_only:
+        r["peak_mb"] = _peak_mb(fwd)
+        r["unfused_peak_mb"] = _peak_mb(lambda: unfused_fwd(x, w1, w2, act))
+    else:
+        r["peak_mb"] = _peak_mb(lambda: (fwd(), bwd()))
+
+        def unfused():
+            o, z, h = unfused_fwd(x, w1, w2, act)
+            return o, unfused_bwd(x, w1, w2, do, z, h, act)
+
+        r["unfused_peak_mb"] = _peak_mb(unfused)
+    r["peak_savings"] = round(1 - r["peak_mb"] / r["unfused_peak_mb"], 4)
+    del x, w1, w2, do
+    torch.cuda.empty_cache()
+    r["cpu_ms"] = _cpu_config_ms(H, B, D, E, act, x_std, fwd_only)
+    r["cpu_note"] = ("CPU oracle (torch fp32 autograd), one head timed and scaled to all, "
+                     f"{len(os.sched_getaffinity(0))} cores")
     return r
 
 
@@ -806,6 +883,9 @@ def main():
         line["memory"] = peak_memory(x, w1, w2, do, act)
         if args.workload == "cfg4" and not args.no_extra:
             line["memory"]["performance_md_shapes"] = module_memory()
+    if "configs" in line and not (args.no_memory or args.no_cpu):
+        for name in CONFIG_PASS:
+            line["configs"][name].update(config_extras(name))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(H, B, D, E, act, x_std)
     print(json.dumps(line), flush=True)
