@@ -80,11 +80,20 @@ int io_of(int dtype) {
   return dtype & ~(FMLP_OUT_F32 | FMLP_DW_HILO | FMLP_BWD_RECOMPUTE | FMLP_BWD_STORE_DZ | FMLP_BWD_NO_DX | FMLP_BWD_NO_DW);
 }
 
-// backward form selection from the dtype flags (plan_bwd's dz_mode)
-// (a partial backward, FMLP_BWD_NO_DX / FMLP_BWD_NO_DW, runs the recompute form's programs)
+// backward form selection from the dtype flags (plan_bwd's dz_mode). A backward without dW
+// (FMLP_BWD_NO_DW) runs the recompute form's dX programs. One without dX (FMLP_BWD_NO_DX) plans
+// as the same call with dX would, and runs that plan's dW programs (E-tile width, B split) alone
+// without storing dZ, so its dw1, dw2 are the full call's bit for bit.
 int dz_mode_of(int dtype) {
-  if (dtype & (FMLP_BWD_RECOMPUTE | FMLP_BWD_NO_DX | FMLP_BWD_NO_DW)) return fmlp::DZ_NEVER;
+  if (dtype & (FMLP_BWD_RECOMPUTE | FMLP_BWD_NO_DW)) return fmlp::DZ_NEVER;
   return (dtype & FMLP_BWD_STORE_DZ) ? fmlp::DZ_FORCE : fmlp::DZ_AUTO;
+}
+
+// workspace bytes a tuned backward with these flags needs under plan p: with FMLP_BWD_NO_DX the
+// dW programs' fp32 partials alone (no dZ, no split dX tiles), with FMLP_BWD_NO_DW none
+size_t plan_ws_bytes(const fmlp::BwdPlan& p, int dtype) {
+  if (dtype & FMLP_BWD_NO_DW) return 0;
+  return (dtype & FMLP_BWD_NO_DX) ? p.dw_ws_bytes : p.ws_bytes;
 }
 size_t elem_bytes(int io) { return io == FMLP_DTYPE_F32 ? 4 : 2; }
 
@@ -322,7 +331,7 @@ FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int
   size_t n = 0;
   for (int act = 0; act < 4; ++act) {
     const size_t w =
-        fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus).ws_bytes;
+        plan_ws_bytes(fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus), dtype);
     if (w > n) n = w;
   }
   return n;
@@ -348,8 +357,14 @@ FMLP_EXPORT int fmlp_bwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int dt
     return ok();
   }
   const fmlp::BwdPlan p = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus);
-  const int64_t v[11] = {p.dz ? 1 : 0, p.nS, p.dx_es, p.dxs_xs, p.dx_first ? 1 : 0, p.n_dw,
-                         p.n_dx, p.n_dxs, (int64_t)p.ws_bytes, act, p.et_w};
+  // what a call with these flags launches: the dW programs alone (FMLP_BWD_NO_DX, no dZ stored)
+  // or the dX programs alone over whole tiles (FMLP_BWD_NO_DW)
+  const bool no_dw = (dtype & FMLP_BWD_NO_DW) != 0, no_dx = (dtype & FMLP_BWD_NO_DX) != 0;
+  const bool part = no_dx || no_dw;
+  const int64_t v[11] = {p.dz && !part ? 1 : 0, no_dw ? 1 : p.nS, p.dx_es, part ? 0 : p.dxs_xs,
+                         p.dx_first ? 1 : 0, no_dw ? 0 : p.n_dw,
+                         no_dx ? 0 : (no_dw ? H * (int64_t)p.dx_tiles_per_head : p.n_dx), part ? 0 : p.n_dxs,
+                         (int64_t)plan_ws_bytes(p, dtype), act, p.et_w};
   for (int i = 0; i < n_info && i < 11; ++i) info[i] = v[i];
   return ok();
 }
@@ -359,6 +374,7 @@ FMLP_EXPORT int fmlp_bwd_stores_dz(int64_t H, int64_t B, int64_t D, int64_t E, i
   if (!tuned_shape(D, E, io_of(dtype))) return 0;  // the generic kernels recompute
   int cus = 0;
   if (num_cus_current(&cus) != FMLP_OK) return 0;
+  if (dtype & (FMLP_BWD_NO_DX | FMLP_BWD_NO_DW)) return 0;  // a partial backward stores no dZ
   return fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus).dz ? 1 : 0;
 }
 
@@ -399,8 +415,9 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
     // workspace fits it; the unsplit recompute form needs none, so a plan always exists
     const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus,
                                               noalloc ? fmlp::kScratchBytes : (size_t)-1);
-    // the dX programs alone (FMLP_BWD_NO_DW) touch no workspace
-    const size_t ws_need = want_dw ? plan.ws_bytes : 0;
+    // the dX programs alone (FMLP_BWD_NO_DW) touch no workspace, the dW programs alone
+    // (FMLP_BWD_NO_DX) only their fp32 partials
+    const size_t ws_need = plan_ws_bytes(plan, dtype);
     void* ws = want_dw ? workspace : nullptr;
     if (ws_need > 0) {
       if (noalloc) {

@@ -1502,6 +1502,7 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
   p.n_dw = H * (long long)p.nE * p.nS;
   p.dx_first = best_dx_first;
   p.ws_bytes = ws_for(p.nS);
+  p.dw_ws_bytes = p.ws_bytes;
   if (p.dxs_xs > 0) {  // the split dX tiles' partials after the dW partials
     p.n_dxs = H * (long long)p.dxs_xs;
     p.dxs_off = (p.ws_bytes + 255) / 256 * 256;

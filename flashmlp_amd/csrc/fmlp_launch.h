@@ -69,6 +69,7 @@ struct BwdPlan {
   int n_xg;            // dxg_kernel workgroups (persistent), stored-dZ form
   size_t dz_off;       // byte offset of dZ in the workspace, stored-dZ form
   size_t ws_bytes;     // fp32 partials when nS > 1, then dZ (H nE 128 Bp io elements) when dz
+  size_t dw_ws_bytes;  // the fp32 partials alone (at offset 0): what the dW programs need by themselves
 };
 
 struct BwdArgs {

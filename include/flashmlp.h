@@ -80,12 +80,14 @@ typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1, FMLP_DTYPE_F32 = 2 } fml
 
 /* OR-ed into the dtype argument of fmlp_bwd / fmlp_bwd_strided / fmlp_bwd_noalloc: the caller
  * needs no dx (FMLP_BWD_NO_DX: dx may be NULL and is not written; only the dW programs run, in
- * the recompute form's plan) or no dw1, dw2 (FMLP_BWD_NO_DW: both may be NULL and are not
- * written; only the dX programs run, with no workspace: fmlp_bwd_workspace_bytes is 0 and
- * `workspace` may be NULL). The results that are computed are bit-identical to the recompute
- * form's (FMLP_BWD_RECOMPUTE) of the same entry point. No counterpart in the reference, whose backward
- * always computes all three: for autograd callers whose input, or whose weights, need no
- * gradient. Both flags together: nothing to compute. */
+ * the plan the same call without the flag takes, storing no dZ, with the fp32 partials of their
+ * B split as the only workspace; dw1, dw2 are bit-identical to that call's; on the generic
+ * kernels, whose B split follows the workspace given, with the same workspace) or no dw1, dw2
+ * (FMLP_BWD_NO_DW: both may be NULL and are not written; only the dX programs of the recompute
+ * form run, with no workspace: fmlp_bwd_workspace_bytes is 0 and `workspace` may be NULL; dx is
+ * bit-identical to the recompute form's, FMLP_BWD_RECOMPUTE, of the same entry point). No
+ * counterpart in the reference, whose backward always computes all three: for autograd callers
+ * whose input, or whose weights, need no gradient. Both flags together: nothing to compute. */
 #define FMLP_BWD_NO_DX 0x1000
 #define FMLP_BWD_NO_DW 0x2000
 
@@ -151,8 +153,9 @@ int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int
 
 /* Bytes of device workspace fmlp_bwd / fmlp_bwd_strided need for these shapes and dtype flags
  * on the current device, whatever the activation (0 when none is needed). Every backward flag
- * can change it (FMLP_DW_HILO, FMLP_BWD_RECOMPUTE, FMLP_BWD_STORE_DZ and FMLP_BWD_NO_DX change
- * the plan; with FMLP_BWD_NO_DW it is 0): query it with the flags of the call it is for. For
+ * can change it (FMLP_DW_HILO, FMLP_BWD_RECOMPUTE and FMLP_BWD_STORE_DZ change the plan,
+ * FMLP_BWD_NO_DX leaves only the dW programs' partials; with FMLP_BWD_NO_DW it is 0): query it
+ * with the flags of the call it is for. For
  * shapes the tuned kernels do not take, it is the fp32 partials of the generic dW programs'
  * B split (16-bit D = 256 with E % 8 == 0: the larger of that and the D = 256 dW programs'
  * split); those calls (and fmlp_bwd_strided calls whose views send a tuned shape to the
@@ -160,7 +163,8 @@ int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int
 size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype);
 
 /* 1 when fmlp_bwd takes the stored-dZ form for these shapes, dtype flags and activation on the
- * current device, else 0 (also for rejected arguments). No counterpart in the reference: for
+ * current device, else 0 (also for rejected arguments and for a partial backward,
+ * FMLP_BWD_NO_DX or FMLP_BWD_NO_DW, which stores none). No counterpart in the reference: for
  * callers planning memory and for benches naming the kernels they time. */
 int fmlp_bwd_stores_dz(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, int act);
 
@@ -169,7 +173,9 @@ int fmlp_bwd_stores_dz(int64_t H, int64_t B, int64_t D, int64_t E, int dtype, in
  * (0/1), B splits of the dW programs, dX programs' in-workgroup E parts, parts of each split
  * ragged dX tile (0: not split), dX programs first (0/1), dW programs, whole-tile dX programs,
  * split-tile dX programs, workspace bytes, the activation's code, and the E-columns per dW
- * program (128 or 64). Also for dense 16-bit D = 256 with E % 8 == 0 (the D = 256 dX and dW
+ * program (128 or 64). With FMLP_BWD_NO_DX or FMLP_BWD_NO_DW it describes what such a call
+ * launches (the dW programs alone, or the dX programs alone over whole tiles) and the workspace
+ * it needs. Also for dense 16-bit D = 256 with E % 8 == 0 (the D = 256 dX and dW
  * programs, one launch each; the split as with an unlimited workspace, which such calls take
  * only as far as their workspace holds). Returns FMLP_OK, or FMLP_ERR_UNSUPPORTED for shapes
  * the generic kernels take. No counterpart in the reference: a diagnostic for tests and

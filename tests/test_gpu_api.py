@@ -264,14 +264,17 @@ def test_fast_path_equals_general_path(monkeypatch, H, B, D, E, dt, act):
     (2, 4096, 128, 512, torch.bfloat16, "silu"),       # tuned kernels, B split of the dW programs
     (8, 4097, 64, 2048, torch.float16, "sigmoid"),     # tuned kernels, B and dX-tile tails
     (3, 300, 32, 45, torch.float16, "leaky_relu"),     # generic kernels
-], ids=["bf16-D128", "fp16-D64-tail", "fp16-D32-generic"])
+    (1, 4096, 128, 1024, torch.bfloat16, "silu"),      # stored dZ, dW programs split unlike the recompute form's
+], ids=["bf16-D128", "fp16-D64-tail", "fp16-D32-generic", "bf16-D128-stored-dz"])
 def test_function_computes_only_the_gradients_autograd_needs(H, B, D, E, dt, act):
     """FlashMLPFunction passes autograd's needs_input_grad down (FMLP_BWD_NO_DX / FMLP_BWD_NO_DW):
-    an input or weights that need no gradient skip the dX or the dW programs, and what is
-    computed is bit-identical to the recompute form's full backward."""
+    an input or weights that need no gradient skip the dX or the dW programs; dW is
+    bit-identical to the full backward's (the dW programs of its plan), dX to the recompute
+    form's (whose dX programs run)."""
     _say(f"[api] partial backward H={H} B={B} D={D} E={E} {dt} act='{act}'")
     x, w1, w2, do = (t.cuda() for t in make_inputs(H, B, D, E, dt, seed=62))
-    dx, dw1, dw2 = fm.flashmlp_bwd(x, w1, w2, do, act, recompute=True)
+    dx = fm.flashmlp_bwd(x, w1, w2, do, act, recompute=True)[0]
+    _, dw1, dw2 = fm.flashmlp_bwd(x, w1, w2, do, act)
     # the input needs no gradient: dW programs only
     w1g, w2g = w1.clone().requires_grad_(True), w2.clone().requires_grad_(True)
     fm.FlashMLPFunction.apply(x, w1g, w2g, act).backward(do)

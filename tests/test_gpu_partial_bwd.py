@@ -6,8 +6,12 @@ For each entry point and flag:
   * the unwanted outputs are passed filled with a sentinel byte pattern and must come back
     unchanged (the header promises they are not written);
   * the wanted outputs are passed filled with NaN bytes and must come back NaN-free and
-    bit-identical to the same entry point's full backward in the recompute form
-    (FMLP_BWD_RECOMPUTE), which the partial backward runs the programs of;
+    bit-identical to the same entry point's full backward: dw1, dw2 of FMLP_BWD_NO_DX to those
+    of the same call without it (the dW programs of that call's plan, whichever form it takes;
+    with FMLP_BWD_RECOMPUTE as well, to the recompute form's), dx of FMLP_BWD_NO_DW to the
+    recompute form's (FMLP_BWD_RECOMPUTE), whose dX programs it runs; two shapes whose plan
+    stores dZ with dW programs of another B split or width than the recompute form's make the
+    difference between the forms observable;
   * with FMLP_BWD_NO_DW no workspace is needed: fmlp_bwd_workspace_bytes is 0 and a NULL
     workspace is accepted, on a shape whose dW programs split B (where the full backward does
     need one).
@@ -84,13 +88,17 @@ CASES = [
     (8, 4097, 64, 2048, torch.float16, "sigmoid", 72, False),    # tuned kernels, tails
     (3, 300, 32, 45, torch.float16, "leaky_relu", 73, False),    # generic kernels (D = 32)
     (2, 260, 64, 136, torch.bfloat16, "silu", 74, True),         # generic kernels (strided X)
+    (1, 4096, 128, 1024, torch.bfloat16, "silu", 75, False),     # stored dZ, another B split
+    (1, 4096, 64, 2048, torch.float16, "sigmoid", 76, False),    # stored dZ, 128- vs 64-column dW
 ]
+STORED = {(1, 4096, 128, 1024), (1, 4096, 64, 2048)}
 ENTRIES = ["fmlp_bwd", "fmlp_bwd_strided", "fmlp_bwd_noalloc"]
 
 
 @pytest.mark.parametrize("entry", ENTRIES)
 @pytest.mark.parametrize("H,B,D,E,dt,act,seed,xt", CASES,
-                         ids=["bf16-D128-split", "fp16-D64-tail", "fp16-D32-generic", "bf16-D64-stridedX"])
+                         ids=["bf16-D128-split", "fp16-D64-tail", "fp16-D32-generic", "bf16-D64-stridedX",
+                              "bf16-D128-stored-dz", "fp16-D64-stored-dz"])
 def test_partial_backward_writes_only_what_is_asked(entry, H, B, D, E, dt, act, seed, xt):
     if xt and entry != "fmlp_bwd_strided":
         pytest.skip("a strided view goes through fmlp_bwd_strided only")
@@ -98,19 +106,35 @@ def test_partial_backward_writes_only_what_is_asked(entry, H, B, D, E, dt, act, 
     if xt:  # same values, X stored as (H, D, B) and viewed as (H, B, D)
         x = x.transpose(1, 2).contiguous().transpose(1, 2)
     _say(f"[partial] {entry} H={H} B={B} D={D} E={E} {dt} act='{act}' strided_x={xt}")
-    ws, n = _workspace(entry, x, w1, _lib.FMLP_BWD_RECOMPUTE)
-    full = tuple(_filled(s, dt, 0xFF) for s in ((H, B, D), (H, D, E), (H, E, D)))
-    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_RECOMPUTE, full, ws, n)
-    for name, t in zip(("dx", "dw1", "dw2"), full):
-        assert not torch.isnan(t).any(), f"full backward left {name} elements unwritten"
+    if (H, B, D, E) in STORED and entry == "fmlp_bwd":
+        L, code = _lib.lib(), _DT[dt]
+        p_own, p_rec = (ctypes.c_int64 * 11)(), (ctypes.c_int64 * 11)()
+        _lib.check(L.fmlp_bwd_plan(H, B, D, E, code, _lib.ACT_CODES[act], p_own, 11), "plan")
+        _lib.check(L.fmlp_bwd_plan(H, B, D, E, code | _lib.FMLP_BWD_RECOMPUTE, _lib.ACT_CODES[act], p_rec, 11),
+                   "plan")
+        # the plan stores dZ, with dW programs of another B split or E-tile width than the recompute form's
+        assert p_own[0] == 1 and (p_own[1], p_own[10]) != (p_rec[1], p_rec[10]), (list(p_own), list(p_rec))
+    full = {}
+    for form in (_lib.FMLP_BWD_RECOMPUTE, 0):
+        ws, n = _workspace(entry, x, w1, form)
+        full[form] = tuple(_filled(s, dt, 0xFF) for s in ((H, B, D), (H, D, E), (H, E, D)))
+        _call(entry, x, w1, w2, do, act, form, full[form], ws, n)
+        for name, t in zip(("dx", "dw1", "dw2"), full[form]):
+            assert not torch.isnan(t).any(), f"full backward (flags {form:#x}) left {name} elements unwritten"
 
-    # dW only: dx is a sentinel-filled buffer that must stay untouched
-    ws, n = _workspace(entry, x, w1, _lib.FMLP_BWD_NO_DX)
-    dx_s = _filled((H, B, D), dt, SENTINEL)
-    dw1, dw2 = _filled((H, D, E), dt, 0xFF), _filled((H, E, D), dt, 0xFF)
-    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DX, (dx_s, dw1, dw2), ws, n)
-    assert bool((dx_s.view(torch.uint8) == SENTINEL).all()), "FMLP_BWD_NO_DX wrote dx"
-    assert torch.equal(dw1, full[1]) and torch.equal(dw2, full[2])
+    # dW only: dx is a sentinel-filled buffer that must stay untouched; dw1, dw2 are those of
+    # the full call with the same other flags
+    for form in (0, _lib.FMLP_BWD_RECOMPUTE):
+        flags = _lib.FMLP_BWD_NO_DX | form
+        # a strided view of a tuned shape runs on the generic kernels, which split B as far as the
+        # workspace holds, while the query sizes the tuned plan's: give them the full call's
+        ws, n = _workspace(entry, x, w1, form if xt else flags)
+        dx_s = _filled((H, B, D), dt, SENTINEL)
+        dw1, dw2 = _filled((H, D, E), dt, 0xFF), _filled((H, E, D), dt, 0xFF)
+        _call(entry, x, w1, w2, do, act, flags, (dx_s, dw1, dw2), ws, n)
+        assert bool((dx_s.view(torch.uint8) == SENTINEL).all()), "FMLP_BWD_NO_DX wrote dx"
+        assert torch.equal(dw1, full[form][1]) and torch.equal(dw2, full[form][2]), f"flags {flags:#x}"
+    own, full = full[0], full[_lib.FMLP_BWD_RECOMPUTE]
 
     # dX only: dw1, dw2 are sentinel-filled and must stay untouched; no workspace at all
     if entry != "fmlp_bwd_noalloc":
@@ -124,9 +148,9 @@ def test_partial_backward_writes_only_what_is_asked(entry, H, B, D, E, dt, act, 
 
     # NULL for the outputs nobody asked for
     dw1, dw2 = _filled((H, D, E), dt, 0xFF), _filled((H, E, D), dt, 0xFF)
-    ws, n = _workspace(entry, x, w1, _lib.FMLP_BWD_NO_DX)
+    ws, n = _workspace(entry, x, w1, 0 if xt else _lib.FMLP_BWD_NO_DX)
     _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DX, (None, dw1, dw2), ws, n)
-    assert torch.equal(dw1, full[1]) and torch.equal(dw2, full[2])
+    assert torch.equal(dw1, own[1]) and torch.equal(dw2, own[2])
     dx = _filled((H, B, D), dt, 0xFF)
     _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DW, (dx, None, None), None, 0)
     assert torch.equal(dx, full[0])
