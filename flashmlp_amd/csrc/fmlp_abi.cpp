@@ -90,9 +90,10 @@ int dz_mode_of(int dtype) {
 }
 
 // workspace bytes a tuned backward with these flags needs under plan p: with FMLP_BWD_NO_DX the
-// dW programs' fp32 partials alone (no dZ, no split dX tiles), with FMLP_BWD_NO_DW none
+// dW programs' fp32 partials alone (no dZ, no split dX tiles), with FMLP_BWD_NO_DW the split
+// ragged dX tiles' partials alone (none when the plan does not split them)
 size_t plan_ws_bytes(const fmlp::BwdPlan& p, int dtype) {
-  if (dtype & FMLP_BWD_NO_DW) return 0;
+  if (dtype & FMLP_BWD_NO_DW) return p.n_dxs > 0 ? p.ws_bytes - p.dxs_off : 0;
   return (dtype & FMLP_BWD_NO_DX) ? p.dw_ws_bytes : p.ws_bytes;
 }
 size_t elem_bytes(int io) { return io == FMLP_DTYPE_F32 ? 4 : 2; }
@@ -316,7 +317,8 @@ FMLP_EXPORT int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, 
 
 FMLP_EXPORT size_t fmlp_bwd_workspace_bytes(int64_t H, int64_t B, int64_t D, int64_t E, int dtype) {
   if (check_shape(H, B, D, E, dtype) != FMLP_OK) return 0;
-  if (dtype & FMLP_BWD_NO_DW) return 0;            // the dX programs alone use no workspace
+  // the generic and D = 256 dX programs alone use no workspace
+  if ((dtype & FMLP_BWD_NO_DW) && !tuned_shape(D, E, io_of(dtype))) return 0;
   int cus = 0;
   if (num_cus_current(&cus) != FMLP_OK) return 0;
   // the generic kernels: the fp32 partials of their dW programs' B split; dense 16-bit D = 256
@@ -358,12 +360,12 @@ FMLP_EXPORT int fmlp_bwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int dt
   }
   const fmlp::BwdPlan p = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus);
   // what a call with these flags launches: the dW programs alone (FMLP_BWD_NO_DX, no dZ stored)
-  // or the dX programs alone over whole tiles (FMLP_BWD_NO_DW)
   const bool no_dw = (dtype & FMLP_BWD_NO_DW) != 0, no_dx = (dtype & FMLP_BWD_NO_DX) != 0;
   const bool part = no_dx || no_dw;
-  const int64_t v[11] = {p.dz && !part ? 1 : 0, no_dw ? 1 : p.nS, p.dx_es, part ? 0 : p.dxs_xs,
-                         p.dx_first ? 1 : 0, no_dw ? 0 : p.n_dw,
-                         no_dx ? 0 : (no_dw ? H * (int64_t)p.dx_tiles_per_head : p.n_dx), part ? 0 : p.n_dxs,
+  // or the dX programs alone (FMLP_BWD_NO_DW, with the split of the ragged tiles when the plan
+  // splits them)
+  const int64_t v[11] = {p.dz && !part ? 1 : 0, no_dw ? 1 : p.nS, p.dx_es, no_dx ? 0 : p.dxs_xs,
+                         p.dx_first ? 1 : 0, no_dw ? 0 : p.n_dw, no_dx ? 0 : p.n_dx, no_dx ? 0 : p.n_dxs,
                          (int64_t)plan_ws_bytes(p, dtype), act, p.et_w};
   for (int i = 0; i < n_info && i < 11; ++i) info[i] = v[i];
   return ok();
@@ -413,12 +415,13 @@ int bwd_impl(const void* x, const void* w1, const void* w2, const void* dout, vo
     if ((st = num_cus_current(&cus))) return st;
     // with a scratch limit the plan only considers B splits (and the stored-dZ form) whose
     // workspace fits it; the unsplit recompute form needs none, so a plan always exists
-    const fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus,
-                                              noalloc ? fmlp::kScratchBytes : (size_t)-1);
-    // the dX programs alone (FMLP_BWD_NO_DW) touch no workspace, the dW programs alone
-    // (FMLP_BWD_NO_DX) only their fp32 partials
+    fmlp::BwdPlan plan = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus,
+                                        noalloc ? fmlp::kScratchBytes : (size_t)-1);
+    // the dW programs alone (FMLP_BWD_NO_DX) need only their fp32 partials, the dX programs
+    // alone (FMLP_BWD_NO_DW) only the split ragged tiles' partials, at the workspace's start
     const size_t ws_need = plan_ws_bytes(plan, dtype);
-    void* ws = want_dw ? workspace : nullptr;
+    if (!want_dw) plan.dxs_off = 0;
+    void* ws = ws_need > 0 ? workspace : nullptr;
     if (ws_need > 0) {
       if (noalloc) {
         e = fmlp::scratch_current_device(&ws);

@@ -1428,14 +1428,22 @@ BwdPlan make_plan(int64_t H, int64_t B, int64_t D, int64_t E, int act, bool hilo
         const bool dxs_fits = rag && (ws_for(eff) + 255) / 256 * 256 + dxs_bytes(des) <= max_ws;
         for (int split = 0; split <= 1; ++split) {
           if (split ? !dxs_fits : fixed_dxs == 1 && dxs_fits) continue;
-          // the split tiles' work, spread over the device, and the launch that sums them
+          // the split tiles' parts are the launch's last workgroups: they fill the time CUs
+          // spend idle before the last of the other programs ends (idle time only comes at the
+          // end of a list schedule), what does not fit there takes a last partial round of at
+          // least one part; then the launch that sums them
           const long long nx = split ? n_dx - H : n_dx;
-          const double extra =
-              split ? (double)H * dxs_xs * (kPlanFixedUs + (tx - kPlanFixedUs) / dxs_xs) / N + kPlanLaunchUs : 0.0;
+          const double tp = kPlanFixedUs + (tx - kPlanFixedUs) / dxs_xs, wp = (double)H * dxs_xs * tp;
           for (int o = 1; o <= 2; ++o) {
             if (order_env && o != order_env) continue;
-            const double t =
-                (o == 1 ? list_makespan(n_dw, tw, nx, tx, N) : list_makespan(nx, tx, n_dw, tw, N)) + red + extra;
+            const double t2 = o == 1 ? list_makespan(n_dw, tw, nx, tx, N) : list_makespan(nx, tx, n_dw, tw, N);
+            double t = t2 + red;
+            if (split) {
+              const double idle = (double)N * t2 - ((double)n_dw * tw + (double)nx * tx);
+              const double over = wp - std::max(0.0, idle);
+              if (over > 0.0) t += std::max(over / (double)N, tp);
+              t += kPlanLaunchUs;
+            }
             if (best_t == 0.0 || t < best_t) {
               best_t = t;
               best_ns = eff;
@@ -1643,23 +1651,28 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
   // FMLP_BWD_UNIFIED (read once per process): 1 (default) = one launch holding both roles,
   // 0 = dW programs (and their reduction), then dX programs, as separate launches
   static const int unified = env_int("FMLP_BWD_UNIFIED", 1);
-  // a partial backward (FMLP_BWD_NO_DX / FMLP_BWD_NO_DW) launches only the programs it needs
-  if (unified && a.want_dx && a.want_dw && p.n_dw > 0 && p.n_dx + p.n_dxs > 0) {
+  // a partial backward (FMLP_BWD_NO_DX / FMLP_BWD_NO_DW) launches only the programs it needs;
+  // the dX programs alone, where the plan splits the ragged last tiles, are the same launch
+  // without dW programs (and the same sum of the parts), so dX is the full call's bit for bit
+  const bool both = a.want_dw && p.n_dw > 0 && p.n_dx + p.n_dxs > 0;
+  if (unified && a.want_dx && (both || (!a.want_dw && p.n_dxs > 0))) {
+    const long long n_dw = a.want_dw ? p.n_dw : 0;
     float* dxs_ws = p.n_dxs > 0 ? (float*)((char*)a.ws + p.dxs_off) : nullptr;
     auto launch_u = [&](auto k) {
       static std::atomic<unsigned long long> lds_set{0};
       hipError_t r = set_lds_once((const void*)k, (int)lds, lds_set);
       if (r != hipSuccess) return r;
-      hipLaunchKernelGGL(k, dim3((unsigned)(p.n_dw + p.n_dx + p.n_dxs)), dim3(DW2_NT), lds, st, (const u16*)a.x,
+      hipLaunchKernelGGL(k, dim3((unsigned)(n_dw + p.n_dx + p.n_dxs)), dim3(DW2_NT), lds, st, (const u16*)a.x,
                          (const u16*)a.w1, (const u16*)a.w2, (const u16*)a.dout, a.dx, a.dw1, a.dw2, (float*)a.ws,
-                         (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, (int)p.n_dw,
+                         (int)a.H, (int)a.B, (int)a.E, p.nE, p.nS, p.rows_per_split, (int)n_dw,
                          p.dx_tiles_per_head, p.dx_first ? 1 : 0, a.out_f32 ? 1 : 0, (int)p.n_dxs, p.dxs_xs,
                          p.dxs_nct, dxs_ws);
       return hipGetLastError();
     };
     e = a.dw_hilo ? launch_u(bwd_kernel<BF16, D, ACT, true, DES, ET>) : launch_u(bwd_kernel<BF16, D, ACT, false, DES, ET>);
     if (e != hipSuccess) return e;
-    if ((e = reduce()) != hipSuccess || p.n_dxs == 0) return e;
+    if (a.want_dw && (e = reduce()) != hipSuccess) return e;
+    if (p.n_dxs == 0) return hipSuccess;
     // the ragged dX tiles' partials: split tile s is head s's last tile
     return launch_tile_reduce(dxs_ws, a.dx, BF16, (int)a.B, D, DX2_ROWS / DES, (int)a.H, p.dx_tiles_per_head,
                               p.dxs_xs, (int)a.H, a.out_f32 ? 1 : 0, st);

@@ -123,10 +123,8 @@ PyObject* fast_bwd(PyObject*, PyObject* const* args, Py_ssize_t nargs) {
     dw1 = at::empty_like(w1);
     dw2 = at::empty_like(w2);
   }
-  // the workspace this call's plan needs (one plan lookup, for its own activation; with
-  // FMLP_BWD_NO_DW none)
+  // the workspace this call's plan needs (one plan lookup, for its own activation)
   auto ws_need = [&](int f) -> size_t {
-    if (f & FMLP_BWD_NO_DW) return 0;
     int64_t info[9];
     if (fmlp_bwd_plan(H, B, D, E, f, act, info, 9) == FMLP_OK) return (size_t)info[8];
     return fmlp_bwd_workspace_bytes(H, B, D, E, f);

@@ -84,8 +84,10 @@ typedef enum { FMLP_DTYPE_F16 = 0, FMLP_DTYPE_BF16 = 1, FMLP_DTYPE_F32 = 2 } fml
  * B split as the only workspace; dw1, dw2 are bit-identical to that call's; on the generic
  * kernels, whose B split follows the workspace given, with the same workspace) or no dw1, dw2
  * (FMLP_BWD_NO_DW: both may be NULL and are not written; only the dX programs of the recompute
- * form run, with no workspace: fmlp_bwd_workspace_bytes is 0 and `workspace` may be NULL; dx is
- * bit-identical to the recompute form's, FMLP_BWD_RECOMPUTE, of the same entry point). No
+ * form run, as in its launch, split ragged last tiles and their sum included, whose fp32
+ * partials are the only workspace: fmlp_bwd_workspace_bytes is 0, and `workspace` may be NULL,
+ * where the plan splits none; dx is bit-identical to the recompute form's, FMLP_BWD_RECOMPUTE,
+ * of the same entry point). No
  * counterpart in the reference, whose backward always computes all three: for autograd callers
  * whose input, or whose weights, need no gradient. Both flags together: nothing to compute. */
 #define FMLP_BWD_NO_DX 0x1000
@@ -154,8 +156,8 @@ int fmlp_fwd_strided(const void* x, const void* w1, const void* w2, void* o, int
 /* Bytes of device workspace fmlp_bwd / fmlp_bwd_strided need for these shapes and dtype flags
  * on the current device, whatever the activation (0 when none is needed). Every backward flag
  * can change it (FMLP_DW_HILO, FMLP_BWD_RECOMPUTE and FMLP_BWD_STORE_DZ change the plan,
- * FMLP_BWD_NO_DX leaves only the dW programs' partials; with FMLP_BWD_NO_DW it is 0): query it
- * with the flags of the call it is for. For
+ * FMLP_BWD_NO_DX leaves only the dW programs' partials, FMLP_BWD_NO_DW only the split ragged dX
+ * tiles' partials, 0 where the plan splits none): query it with the flags of the call it is for. For
  * shapes the tuned kernels do not take, it is the fp32 partials of the generic dW programs'
  * B split (16-bit D = 256 with E % 8 == 0: the larger of that and the D = 256 dW programs'
  * split); those calls (and fmlp_bwd_strided calls whose views send a tuned shape to the

@@ -12,9 +12,10 @@ For each entry point and flag:
     recompute form's (FMLP_BWD_RECOMPUTE), whose dX programs it runs; two shapes whose plan
     stores dZ with dW programs of another B split or width than the recompute form's make the
     difference between the forms observable;
-  * with FMLP_BWD_NO_DW no workspace is needed: fmlp_bwd_workspace_bytes is 0 and a NULL
-    workspace is accepted, on a shape whose dW programs split B (where the full backward does
-    need one).
+  * with FMLP_BWD_NO_DW the workspace is at most the split ragged dX tiles' partials (the dX
+    programs run as in the recompute form's launch, split parts and their sum included): none,
+    and a NULL workspace is accepted, on a shape whose dW programs split B but whose dX tiles
+    are whole (where the full backward does need one).
 No counterpart in the reference, whose backward always computes all three gradients.
 """
 import ctypes
@@ -136,12 +137,15 @@ def test_partial_backward_writes_only_what_is_asked(entry, H, B, D, E, dt, act, 
         assert torch.equal(dw1, full[form][1]) and torch.equal(dw2, full[form][2]), f"flags {flags:#x}"
     own, full = full[0], full[_lib.FMLP_BWD_RECOMPUTE]
 
-    # dX only: dw1, dw2 are sentinel-filled and must stay untouched; no workspace at all
+    # dX only: dw1, dw2 are sentinel-filled and must stay untouched; the workspace holds at most
+    # the split ragged tiles' partials
+    ws, n = _workspace(entry, x, w1, _lib.FMLP_BWD_NO_DW)
     if entry != "fmlp_bwd_noalloc":
-        assert _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, _DT[dt] | _lib.FMLP_BWD_NO_DW) == 0
+        full_n = _lib.lib().fmlp_bwd_workspace_bytes(H, B, D, E, _DT[dt] | _lib.FMLP_BWD_RECOMPUTE)
+        assert n <= full_n, (n, full_n)
     dx = _filled((H, B, D), dt, 0xFF)
     dw1_s, dw2_s = _filled((H, D, E), dt, SENTINEL), _filled((H, E, D), dt, SENTINEL)
-    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DW, (dx, dw1_s, dw2_s), None, 0)
+    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DW, (dx, dw1_s, dw2_s), ws, n)
     assert bool((dw1_s.view(torch.uint8) == SENTINEL).all()), "FMLP_BWD_NO_DW wrote dw1"
     assert bool((dw2_s.view(torch.uint8) == SENTINEL).all()), "FMLP_BWD_NO_DW wrote dw2"
     assert torch.equal(dx, full[0])
@@ -152,7 +156,8 @@ def test_partial_backward_writes_only_what_is_asked(entry, H, B, D, E, dt, act, 
     _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DX, (None, dw1, dw2), ws, n)
     assert torch.equal(dw1, own[1]) and torch.equal(dw2, own[2])
     dx = _filled((H, B, D), dt, 0xFF)
-    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DW, (dx, None, None), None, 0)
+    ws, n = _workspace(entry, x, w1, _lib.FMLP_BWD_NO_DW)
+    _call(entry, x, w1, w2, do, act, _lib.FMLP_BWD_NO_DW, (dx, None, None), ws, n)
     assert torch.equal(dx, full[0])
 
 
