@@ -93,6 +93,7 @@ int dz_mode_of(int dtype) {
 // dW programs' fp32 partials alone (no dZ, no split dX tiles), with FMLP_BWD_NO_DW the split
 // ragged dX tiles' partials alone (none when the plan does not split them)
 size_t plan_ws_bytes(const fmlp::BwdPlan& p, int dtype) {
+  if ((dtype & FMLP_BWD_NO_DX) && (dtype & FMLP_BWD_NO_DW)) return 0;  // nothing to compute
   if (dtype & FMLP_BWD_NO_DW) return p.n_dxs > 0 ? p.ws_bytes - p.dxs_off : 0;
   return (dtype & FMLP_BWD_NO_DX) ? p.dw_ws_bytes : p.ws_bytes;
 }
