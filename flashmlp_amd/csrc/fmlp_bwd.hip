@@ -1073,35 +1073,47 @@ dw_reduce_kernel(const float* __restrict__ ws, void* __restrict__ dW1, void* __r
 // ------------------------------------------------------------------------------------
 // dX from the stored dZ (dxg_kernel): dX = dZ W1^T per head, a GEMM over E, when the dW
 // programs store dZ (the io-dtype value the reference's dX product takes,
-// flashmlp.py:227-235) instead of the dX programs recomputing Z and dH. A tile is 256 rows
-// of one head (one contiguous block of dZ, chunk after chunk), 8 waves x 32 rows; per 32-column
+// flashmlp.py:227-235) instead of the dX programs recomputing Z and dH. A tile is TP blocks of
+// 256 rows of one head (a block is one contiguous run of dZ, chunk after chunk), 8 waves x 32
+// rows of each block; per 32-column
 // E-chunk c a wave issues D/16 MFMAs dX^T += W1c(c) dZ(c)^T (the transposed product: each lane
 // ends with whole row pieces of dX; a lane swap makes each bf16/fp16 store 16 bytes).
 // Persistent: one workgroup per CU walks its tiles as one stream of (tile, chunk) steps, so
 // the loads run ahead across tile boundaries and no tile pays the memory latency up front.
-// LDS: a ring of dZ chunks (8 blocks [32 e][32 positions], 64-byte rows; block w = wave w's
-// rows, read with ds_read_b64_tr_b16 like a row-major [e][b] tile) streamed from HBM 7 steps
-// ahead, and a ring of W1c chunks ([D][32], 64-byte rows, 16-byte chunk q of row r at
+// LDS: a ring of dZ chunks (per 256-row block 8 sub-blocks [32 e][32 positions], 64-byte rows;
+// sub-block w = wave w's rows, read with ds_read_b64_tr_b16 like a row-major [e][b] tile)
+// streamed from HBM (TP = 1: 8 slots 7 steps ahead), and a ring of W1c chunks ([D][32], 64-byte rows, 16-byte chunk q of row r at
 // q ^ ((r >> 2) & 3), read row-wise; L2-resident) 3 steps ahead. One barrier per step.
 // Stored positions are sig-permuted within 16 rows: the lane holding position m holds row sig(m).
 // ------------------------------------------------------------------------------------
-constexpr int DXG_ZS = 8;  // dZ chunk ring slots (16 KB each)
-constexpr int DXG_ZPF = 7; // dZ chunks requested ahead: step j + 7 reuses the slot of step j - 1
+// TP = 2 (the default): a tile is two consecutive 256-row blocks of one head, so each W1c chunk
+// (and each W1c operand read from LDS) serves both: half the W1c traffic, which a copy of the
+// kernel with no W1c traffic priced at 33 us of the cfg4 backward; a step then loads two 16 KB
+// dZ chunks into a 32 KB slot of a 4-slot ring three steps ahead, and a wave keeps two
+// accumulator sets (190 VGPRs at D = 128). Measured at cfg4: backward 787 -> 763 us, step
+// +1.7 % (same box, 3 rounds each).
+__host__ __device__ constexpr int dxg_zs(int TP) { return TP == 1 ? 8 : 4; }  // dZ ring slots (TP x 16 KB each)
+__host__ __device__ constexpr int dxg_zpf(int TP) { return dxg_zs(TP) - 1; }  // step j + ZPF reuses the slot of step j - 1
+constexpr int DXG_ZS = dxg_zs(1);
 constexpr int DXG_WS = 4;  // W1c ring slots (64 D bytes each)
 constexpr int DXG_WPF = 3;
-static_assert(DXG_ZPF <= DXG_ZS - 1 && DXG_WPF <= DXG_WS - 1 && DXG_WPF <= DXG_ZPF, "rings");
+static_assert(DXG_WPF <= DXG_WS - 1 && DXG_WPF <= dxg_zpf(2), "rings");
 
-template <bool BF16, int D>
+template <bool BF16, int D, int TP = 1>
 __global__ void __launch_bounds__(DX2_NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __restrict__ dX, int B, int Bp, int E,
            int Ep, int tiles_per_head, int n_tiles, int outf32) {
+  static_assert(TP == 1 || TP == 2, "256-row blocks per tile");
   constexpr int NTN = D / 32;
-  constexpr int ZT = 32 * 256 * 2;      // dZ chunk bytes
-  constexpr int WOFF = DXG_ZS * ZT;     // W1c ring after the dZ ring
+  constexpr int ZT = 32 * 256 * 2;      // dZ chunk bytes of one 256-row block
+  constexpr int ZS = dxg_zs(TP), ZPF = dxg_zpf(TP);
+  constexpr int ZTS = TP * ZT;          // dZ slot bytes
+  constexpr int WOFF = ZS * ZTS;        // W1c ring after the dZ ring
   constexpr int WT = 64 * D;            // W1c chunk bytes
-  constexpr int NZ = ZT / 16 / DX2_NT;  // dZ pieces per lane per chunk (2)
+  constexpr int NZ = ZT / 16 / DX2_NT;  // dZ pieces per lane per block chunk (2)
   constexpr int W1W = D / 16;           // waves whose lanes cover W1c's 4 D pieces once (the rest repeat them)
   static_assert(NZ * 16 * DX2_NT == ZT, "dZ pieces");
+  const int nblk = Bp / DX2_ROWS;       // 256-row blocks per head
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1111,7 +1123,7 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
   const int my_tiles = wg < n_tiles ? (n_tiles - 1 - wg) / nwg + 1 : 0;
   const int steps = my_tiles * NC;
   // tile k of this workgroup: virtual index v = k * nwg + wg, taken in descending row order over
-  // all heads (v = 0 .. H - 1 are the last 256-row tiles of heads 0 .. H - 1). The dW programs
+  // all heads (v = 0 .. H - 1 are the last tiles of heads 0 .. H - 1). The dW programs
   // walk their rows upwards, so the dZ they stored last is read first, while the device's
   // memory-side cache still holds it (measured at cfg4: 288 -> 270 us). When nwg is a multiple
   // of H (cfg4: 256 and 32), workgroup wg serves head wg mod H only, on XCD wg mod 8 (the
@@ -1137,15 +1149,17 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
   // resources), so every step issues the same number of loads and the vmcnt waits stay exact.
   // Each request stream keeps its own cursor; the tile's addresses change only between tiles.
   struct Cursor {
-    int j, k, c;
-    const u16* z;  // dZ chunk c of tile k
+    int j, k, c, nb;
+    const u16* z;  // dZ chunk c of tile k's first block
     const u16* w;  // W1 columns 32 c .. of tile k's head
   };
   auto seek = [&](Cursor& q) {  // q.k changed: the new tile's base addresses
     const int t = q.k < my_tiles ? tile_of(q.k) : 0;
     const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
-    q.z = dzt + ((size_t)h * Bp + (size_t)bt * DX2_ROWS) * Ep;  // the tile's chunks, 8192 elements each
+    // the tile's blocks' chunks, 8192 elements each, block after block
+    q.z = dzt + ((size_t)h * Bp + (size_t)bt * TP * DX2_ROWS) * Ep;
     q.w = W1 + (size_t)h * D * E;
+    q.nb = min(TP, nblk - bt * TP);  // blocks of the tile within the head (TP = 2: the last may hold one)
   };
   auto advance = [&](Cursor& q) {
     ++q.j;
@@ -1159,11 +1173,14 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
     }
   };
   auto dma_z = [&](const Cursor& q) {
-    const i32x4 rz = make_rsrc_words(q.z, q.k < my_tiles ? 32 * 512 : 0);
-    const int base = (q.j & (DXG_ZS - 1)) * ZT;
 #pragma unroll
-    // the one read of each dZ block: non-temporal (step +0.5-1 % at cfg4 over cached loads)
-    for (int i = 0; i < NZ; ++i) buf_load16_lds_nt(rz, zOff[i], base + (i * DX2_NT + wave * 64) * 16);
+    for (int tp = 0; tp < TP; ++tp) {
+      const i32x4 rz = make_rsrc_words(q.z + (size_t)tp * DX2_ROWS * Ep, q.k < my_tiles && tp < q.nb ? ZT : 0);
+      const int base = (q.j & (ZS - 1)) * ZTS + tp * ZT;
+#pragma unroll
+      // the one read of each dZ block: non-temporal (step +0.5-1 % at cfg4 over cached loads)
+      for (int i = 0; i < NZ; ++i) buf_load16_lds_nt(rz, zOff[i], base + (i * DX2_NT + wave * 64) * 16);
+    }
   };
   auto dma_w = [&](const Cursor& q) {
     const int lim = E - q.c * 32;
@@ -1179,18 +1196,20 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
 #pragma unroll
   for (int s2 = 0; s2 < 2; ++s2) offB[s2] = WOFF + l32 * 64 + (((2 * s2 + g) ^ ((l32 >> 2) & 3)) << 4);
 
-  f32x16 acc[NTN];
+  f32x16 acc[TP][NTN];
 #pragma unroll
-  for (int nt = 0; nt < NTN; ++nt) acc[nt] = zero16();
+  for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+    for (int nt = 0; nt < NTN; ++nt) acc[tp][nt] = zero16();
 
-  // step i requests dZ of step i + DXG_ZPF, then W1c of step i + DXG_WPF; the prologue runs the
+  // step i requests dZ of step i + ZPF, then W1c of step i + DXG_WPF; the prologue runs the
   // same order for i < 0, so at step j the loads issued after W1c(j) are those of steps
   // j - 2 .. j - 1 (DXG_WPF - 1 of them)
-  Cursor qz{0, 0, 0, nullptr, nullptr};
+  Cursor qz{0, 0, 0, 0, nullptr, nullptr};
   seek(qz);
   Cursor qw = qz;
 #pragma unroll
-  for (int i = -DXG_ZPF; i < 0; ++i) {
+  for (int i = -ZPF; i < 0; ++i) {
     dma_z(qz);
     advance(qz);
     if (i + DXG_WPF >= 0) {
@@ -1204,10 +1223,10 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
     // this wave's pieces of step j (dZ and W1c) have landed: the loads of steps j - 2, j - 1 may
     // stay in flight and, when a tile ended in steps j - 3 .. j - 1 (one at most when NC >= 3),
     // that tile's stores, issued after W1c(j) (vmcnt counts loads and stores in issue order)
-    constexpr int NW0 = (NZ + 1) * (DXG_WPF - 1);
+    constexpr int NW0 = (TP * NZ + 1) * (DXG_WPF - 1);
     if (++since <= DXG_WPF && NC >= DXG_WPF) {
-      if (outf32) wait_vmcnt<NW0 + 4 * NTN>();
-      else wait_vmcnt<NW0 + 2 * NTN>();
+      if (outf32) wait_vmcnt<NW0 + TP * 4 * NTN>();
+      else wait_vmcnt<NW0 + TP * 2 * NTN>();
     } else {
       wait_vmcnt<NW0>();
     }
@@ -1219,11 +1238,13 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
     advance(qz);
     dma_w(qw);
     advance(qw);
-    const int zb = (j & (DXG_ZS - 1)) * ZT, wb = (j & (DXG_WS - 1)) * WT;
-    u32x4 a[2], b[2][NTN];
+    const int zb = (j & (ZS - 1)) * ZTS, wb = (j & (DXG_WS - 1)) * WT;
+    u32x4 a[TP][2], b[2][NTN];
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
-      a[s2] = cat(lds_read_tr(zb + laneA + s2 * 1024), lds_read_tr(zb + laneA + s2 * 1024 + 256));
+#pragma unroll
+      for (int tp = 0; tp < TP; ++tp)
+        a[tp][s2] = cat(lds_read_tr(zb + tp * ZT + laneA + s2 * 1024), lds_read_tr(zb + tp * ZT + laneA + s2 * 1024 + 256));
 #pragma unroll
       for (int nt = 0; nt < NTN; ++nt) b[s2][nt] = lds_read16(wb + offB[s2] + nt * 2048);
     }
@@ -1231,46 +1252,55 @@ dxg_kernel(const u16* __restrict__ dzt, const u16* __restrict__ W1, void* __rest
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2)
 #pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) acc[nt] = mfma<BF16>(b[s2][nt], a[s2], acc[nt]);
-    if (++c == NC) {  // tile done: lane l32 holds row sig(l32) of the wave's 32, columns
-                      // 32 nt + 8 q + 4 g + 0..3 in acc[nt][4 q .. 4 q + 3]: 16-byte buffer
-                      // stores, rows past B out of range
+      for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) acc[tp][nt] = mfma<BF16>(b[s2][nt], a[tp][s2], acc[tp][nt]);
+    if (++c == NC) {  // tile done: lane l32 holds row sig(l32) of the wave's 32 in each block,
+                      // columns 32 nt + 8 q + 4 g + 0..3 in acc[tp][nt][4 q .. 4 q + 3]: 16-byte
+                      // buffer stores, rows past B out of range
       const int t = tile_of(k);  // once per tile
       const int h = t / tiles_per_head, bt = t - h * tiles_per_head;
-      const int rows = clamp0(B - bt * DX2_ROWS, DX2_ROWS);
       const unsigned r = (unsigned)(wave * 32) + sig((unsigned)l32);
-      if (outf32) {
-        const Rsrc ro = make_rsrc((const float*)dX + ((size_t)h * B + (size_t)bt * DX2_ROWS) * D, rows * D * 4);
 #pragma unroll
-        for (int nt = 0; nt < NTN; ++nt)
+      for (int tp = 0; tp < TP; ++tp) {
+        const int blk = bt * TP + tp;
+        const int rows = clamp0(B - blk * DX2_ROWS, DX2_ROWS);
+        if (outf32) {
+          const Rsrc ro = make_rsrc((const float*)dX + ((size_t)h * B + (size_t)blk * DX2_ROWS) * D, rows * D * 4);
 #pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const u32x4 v = {__float_as_uint(acc[nt][4 * q]), __float_as_uint(acc[nt][4 * q + 1]),
-                             __float_as_uint(acc[nt][4 * q + 2]), __float_as_uint(acc[nt][4 * q + 3])};
-            __builtin_amdgcn_raw_buffer_store_b128(v, ro, (int)((r * D + 32 * nt + 8 * q + 4 * g) * 4u), 0, 0);
-          }
-      } else {
-        const Rsrc ro = make_rsrc((const u16*)dX + ((size_t)h * B + (size_t)bt * DX2_ROWS) * D, rows * D * 2);
+          for (int nt = 0; nt < NTN; ++nt)
 #pragma unroll
-        for (int nt = 0; nt < NTN; ++nt) {
-          u32x2 v[4];
+            for (int q = 0; q < 4; ++q) {
+              const u32x4 v = {__float_as_uint(acc[tp][nt][4 * q]), __float_as_uint(acc[tp][nt][4 * q + 1]),
+                               __float_as_uint(acc[tp][nt][4 * q + 2]), __float_as_uint(acc[tp][nt][4 * q + 3])};
+              __builtin_amdgcn_raw_buffer_store_b128(v, ro, (int)((r * D + 32 * nt + 8 * q + 4 * g) * 4u), 0, 0);
+            }
+        } else {
+          const Rsrc ro = make_rsrc((const u16*)dX + ((size_t)h * B + (size_t)blk * DX2_ROWS) * D, rows * D * 2);
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            v[q] = u32x2{pack2<BF16>(acc[nt][4 * q], acc[nt][4 * q + 1]), pack2<BF16>(acc[nt][4 * q + 2], acc[nt][4 * q + 3])};
+          for (int nt = 0; nt < NTN; ++nt) {
+            u32x2 v[4];
 #pragma unroll
-          for (int p = 0; p < 2; ++p) {
-            // lanes 0-31 hold columns 8q + 0..3, lanes 32-63 8q + 4..7: one swap gives lane g
-            // columns 16 p + 8 g .. + 7
-            const auto s0 = __builtin_amdgcn_permlane32_swap(v[2 * p][0], v[2 * p + 1][0], false, false);
-            const auto s1 = __builtin_amdgcn_permlane32_swap(v[2 * p][1], v[2 * p + 1][1], false, false);
-            const u32x4 w = {s0[0], s1[0], s0[1], s1[1]};
-            __builtin_amdgcn_raw_buffer_store_b128(w, ro, (int)((r * D + 32 * nt + 16 * p + 8 * g) * 2u), 0, 0);
+            for (int q = 0; q < 4; ++q)
+              v[q] = u32x2{pack2<BF16>(acc[tp][nt][4 * q], acc[tp][nt][4 * q + 1]),
+                           pack2<BF16>(acc[tp][nt][4 * q + 2], acc[tp][nt][4 * q + 3])};
+#pragma unroll
+            for (int p = 0; p < 2; ++p) {
+              // lanes 0-31 hold columns 8q + 0..3, lanes 32-63 8q + 4..7: one swap gives lane g
+              // columns 16 p + 8 g .. + 7
+              const auto s0 = __builtin_amdgcn_permlane32_swap(v[2 * p][0], v[2 * p + 1][0], false, false);
+              const auto s1 = __builtin_amdgcn_permlane32_swap(v[2 * p][1], v[2 * p + 1][1], false, false);
+              const u32x4 w = {s0[0], s1[0], s0[1], s1[1]};
+              __builtin_amdgcn_raw_buffer_store_b128(w, ro, (int)((r * D + 32 * nt + 16 * p + 8 * g) * 2u), 0, 0);
+            }
           }
         }
       }
       since = 0;
 #pragma unroll
-      for (int nt = 0; nt < NTN; ++nt) acc[nt] = zero16();
+      for (int tp = 0; tp < TP; ++tp)
+#pragma unroll
+        for (int nt = 0; nt < NTN; ++nt) acc[tp][nt] = zero16();
       c = 0;
       ++k;
     }
@@ -1640,13 +1670,21 @@ static hipError_t launch_bwd_t(const BwdArgs& a, const BwdPlan& p, hipStream_t s
     e = a.dw_hilo ? launch_w(dw2_kernel<BF16, D, ACT, true, true>) : launch_w(dw2_kernel<BF16, D, ACT, false, true>);
     if (e != hipSuccess) return e;
     if ((e = reduce()) != hipSuccess) return e;
-    const size_t lds_g = (size_t)DXG_ZS * (32 * 256 * 2) + (size_t)DXG_WS * 64 * D;
-    auto kg = dxg_kernel<BF16, D>;
-    static std::atomic<unsigned long long> lds_g_set{0};
-    if ((e = set_lds_once((const void*)kg, (int)lds_g, lds_g_set)) != hipSuccess) return e;
-    hipLaunchKernelGGL(kg, dim3((unsigned)p.n_xg), dim3(DX2_NT), lds_g, st, (const u16*)dzt, (const u16*)a.w1, a.dx,
-                       (int)a.B, p.Bp, (int)a.E, Ep, p.Bp / DX2_ROWS, (int)p.n_dx, a.out_f32 ? 1 : 0);
-    return hipGetLastError();
+    // FMLP_DXG_TP (read once per process): 256-row blocks per dX GEMM tile, 2 (default) or 1
+    static const int tp_env = env_int("FMLP_DXG_TP", 2);
+    auto launch_g = [&](auto kg, int TP) {
+      static std::atomic<unsigned long long> lds_g_set[2] = {};
+      const size_t lds_g = (size_t)dxg_zs(TP) * TP * (32 * 256 * 2) + (size_t)DXG_WS * 64 * D;
+      hipError_t r = set_lds_once((const void*)kg, (int)lds_g, lds_g_set[TP - 1]);
+      if (r != hipSuccess) return r;
+      const int tph = (p.Bp / DX2_ROWS + TP - 1) / TP;  // tiles per head
+      const long long n_t = a.H * (long long)tph;
+      const long long grid = TP == 1 ? p.n_xg : std::min<long long>(n_t, p.n_xg);
+      hipLaunchKernelGGL(kg, dim3((unsigned)grid), dim3(DX2_NT), lds_g, st, (const u16*)dzt, (const u16*)a.w1, a.dx,
+                         (int)a.B, p.Bp, (int)a.E, Ep, tph, (int)n_t, a.out_f32 ? 1 : 0);
+      return hipGetLastError();
+    };
+    return tp_env == 1 ? launch_g(dxg_kernel<BF16, D, 1>, 1) : launch_g(dxg_kernel<BF16, D, 2>, 2);
   }
   // FMLP_BWD_UNIFIED (read once per process): 1 (default) = one launch holding both roles,
   // 0 = dW programs (and their reduction), then dX programs, as separate launches
