@@ -364,7 +364,7 @@ def host_us_per_call(fn, n=200):
     return (t1 - t0) / n * 1e6
 
 
-def autograd_step_ms(x, w1, w2, do, act, warmup=3, iters=20):
+def autograd_step_ms(x, w1, w2, do, act, warmup=5, iters=50):
     """Module-level training step as example.py:120-128 times it: FlashMLPFunction forward
     on a leaf that requires grad, then backward (here with dO, the bench's gradient)."""
     import flashmlp_amd as fm
