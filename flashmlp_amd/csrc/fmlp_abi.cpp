@@ -361,10 +361,10 @@ FMLP_EXPORT int fmlp_bwd_plan(int64_t H, int64_t B, int64_t D, int64_t E, int dt
   }
   const fmlp::BwdPlan p = fmlp::plan_bwd(H, B, D, E, act, (dtype & FMLP_DW_HILO) != 0, dz_mode_of(dtype), cus);
   // what a call with these flags launches: the dW programs alone (FMLP_BWD_NO_DX, no dZ stored)
-  const bool no_dw = (dtype & FMLP_BWD_NO_DW) != 0, no_dx = (dtype & FMLP_BWD_NO_DX) != 0;
-  const bool part = no_dx || no_dw;
   // or the dX programs alone (FMLP_BWD_NO_DW, with the split of the ragged tiles when the plan
   // splits them)
+  const bool no_dw = (dtype & FMLP_BWD_NO_DW) != 0, no_dx = (dtype & FMLP_BWD_NO_DX) != 0;
+  const bool part = no_dx || no_dw;
   const int64_t v[11] = {p.dz && !part ? 1 : 0, no_dw ? 1 : p.nS, p.dx_es, no_dx ? 0 : p.dxs_xs,
                          p.dx_first ? 1 : 0, no_dw ? 0 : p.n_dw, no_dx ? 0 : p.n_dx, no_dx ? 0 : p.n_dxs,
                          (int64_t)plan_ws_bytes(p, dtype), act, p.et_w};

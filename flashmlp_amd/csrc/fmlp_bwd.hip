@@ -1082,8 +1082,9 @@ dw_reduce_kernel(const float* __restrict__ ws, void* __restrict__ dW1, void* __r
 // the loads run ahead across tile boundaries and no tile pays the memory latency up front.
 // LDS: a ring of dZ chunks (per 256-row block 8 sub-blocks [32 e][32 positions], 64-byte rows;
 // sub-block w = wave w's rows, read with ds_read_b64_tr_b16 like a row-major [e][b] tile)
-// streamed from HBM (TP = 1: 8 slots 7 steps ahead), and a ring of W1c chunks ([D][32], 64-byte rows, 16-byte chunk q of row r at
-// q ^ ((r >> 2) & 3), read row-wise; L2-resident) 3 steps ahead. One barrier per step.
+// streamed from HBM (TP = 1: 8 slots 7 steps ahead), and a ring of W1c chunks ([D][32],
+// 64-byte rows, 16-byte chunk q of row r at q ^ ((r >> 2) & 3), read row-wise; L2-resident)
+// 3 steps ahead. One barrier per step.
 // Stored positions are sig-permuted within 16 rows: the lane holding position m holds row sig(m).
 // ------------------------------------------------------------------------------------
 // TP = 2 (the default): a tile is two consecutive 256-row blocks of one head, so each W1c chunk
