@@ -56,7 +56,7 @@ SIGNATURES = {
                                         ctypes.c_int, _vp]),
 }
 FMLP_SCRATCH_MAX_BYTES = 64 << 20
-ABI_VERSION = 3  # FMLP_ABI_VERSION of include/flashmlp.h
+ABI_VERSION = 4  # FMLP_ABI_VERSION of include/flashmlp.h
 
 _lock = threading.Lock()
 _lib = None

@@ -36,7 +36,10 @@
 extern "C" {
 #endif
 
-#define FMLP_ABI_VERSION 3  /* 2: FMLP_BWD_NO_DX / FMLP_BWD_NO_DW; 3: fmlp_fwd_ws, fmlp_bwd_plan */
+#define FMLP_ABI_VERSION 4  /* 2: FMLP_BWD_NO_DX / FMLP_BWD_NO_DW; 3: fmlp_fwd_ws, fmlp_bwd_plan;
+                              4: FMLP_BWD_NO_DX runs the full call's dW plan, FMLP_BWD_NO_DW
+                              the full recompute launch's dX programs (a workspace where it
+                              splits ragged dX tiles) */
 
 typedef enum {
   FMLP_OK = 0,

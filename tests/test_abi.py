@@ -44,7 +44,7 @@ def test_library_exports_every_declared_symbol(L):
 
 
 def test_version_and_status_strings(L):
-    assert L.fmlp_abi_version() == 3
+    assert L.fmlp_abi_version() == 4
     assert L.fmlp_status_string(OK) == b"ok"
     for st in (INVALID, UNSUPPORTED, HIPERR, WORKSPACE):
         assert L.fmlp_status_string(st) not in (b"ok", b"unknown status")
